@@ -1,0 +1,144 @@
+/*
+ * lbw_attn.h -- C ABI of the MI355X (gfx950) causal-chunk attention path.
+ *
+ * Plain pointers and sizes only (no torch types). Every tensor pointer is a device pointer.
+ * Element strides are in elements of the tensor's own type; the innermost (head_dim)
+ * dimension is always contiguous. Every entry point returns 0 (LBW_OK) on success and a
+ * nonzero LBW_ERR_* code otherwise, with a message in lbw_last_error() (per thread).
+ * All work is enqueued on `stream` (a hipStream_t; NULL = the default stream) and is
+ * asynchronous; nothing here synchronises the device or allocates memory.
+ *
+ * Reference interfaces replaced (paths inside the reference repository):
+ *   lbw_attention_fwd      wan/modules/attention.py:1082-1143  attention(q, k, v, ...)
+ *                          wan/modules/attention.py:1048-1058  exact_attention_chunks
+ *                          wan/modules/attention.py:617-645    cte_partial (partials mode)
+ *                          kernels/self_attention_nst.py:49    wan_flash_self_attn
+ *                          kernels/attention_cte_lb.py:270     attention_cte
+ *   lbw_cross_attention_fwd wan/modules/attention.py:280-311   _nki_cross_attention
+ *                          kernels/cross_attention.py:17       wan_cross_attn
+ *   lbw_attn_merge         wan/modules/attention.py:963-990    cte_merge
+ *   lbw_qk_norm_rope       kernels/qk_post.py:404-413          qk_ss + qk_norm_rope
+ *                          (caller wan/modules/model_fast.py:2596-2681 _qkv_post)
+ *   lbw_kv_quant_fp8       no reference counterpart (new fp8-e4m3 KV cache)
+ *   lbw_attention_fwd_fp8kv no reference counterpart; nearest is the delayed fp8 K
+ *                          dequant of kernels/attention_cte_lb.py:645-647
+ */
+#ifndef LBW_ATTN_H
+#define LBW_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LBW_ABI_VERSION 1
+#define LBW_MAX_KV_SEGMENTS 8
+#define LBW_FP8_BLOCK 64
+
+enum {
+  LBW_OK = 0,
+  LBW_ERR_INVALID = 1,     /* bad argument (shape, stride, pointer, size) */
+  LBW_ERR_UNSUPPORTED = 2, /* valid but not implemented here (e.g. head_dim != 128) */
+  LBW_ERR_HIP = 3,         /* a HIP runtime call failed */
+  LBW_ERR_WORKSPACE = 4    /* workspace missing or too small */
+};
+
+/* One contiguous piece of the KV sequence, tokens-major [B, len, H, D]. The attention sees
+ * the concatenation of the segments in order (e.g. the cached frames then the current
+ * chunk, or the chunked cache's (leading..., destination) buffers), without a copy. */
+typedef struct lbw_kv_segment {
+  const void* k;        /* bf16, or e4m3fn codes (uint8) for the fp8 entry point */
+  const void* v;
+  int64_t len;          /* tokens in this segment */
+  int64_t k_stride_b, k_stride_l, k_stride_h;
+  int64_t v_stride_b, v_stride_l, v_stride_h;
+  const float* k_scale; /* fp8 only: [B, H, ceil(len / 64)] fp32, contiguous */
+  const float* v_scale;
+} lbw_kv_segment;
+
+typedef struct lbw_attn_params {
+  int32_t batch, heads, head_dim, lq;
+  const void* q;        /* bf16 [B, Lq, H, D] */
+  int64_t q_stride_b, q_stride_l, q_stride_h;
+  void* out;            /* bf16 [B, Lq, H, D]; may be NULL when partials are requested */
+  int64_t o_stride_b, o_stride_l, o_stride_h;
+  int32_t n_segments;
+  lbw_kv_segment seg[LBW_MAX_KV_SEGMENTS];
+  int64_t kv_lo, kv_hi; /* window [kv_lo, kv_hi) over the concatenated keys; kv_hi < 0: all */
+  const int32_t* k_lens;/* device int32 [B] valid key counts (masked cross-attention) or NULL */
+  float softmax_scale;  /* <= 0: 1 / sqrt(head_dim) */
+  int32_t num_splits;   /* KV splits merged by log-sum-exp; 0 = choose, 1 = single pass */
+  /* Optional cte_partial outputs, fp32 and contiguous: O_unnorm [B, H, Lq, D],
+   * m [B, H, Lq] (row max of the scaled scores), l [B, H, Lq] (row sum of exp(s - m)).
+   * When set, the normalised `out` is not written and num_splits must be 1. */
+  float* part_o;
+  float* part_m;
+  float* part_l;
+} lbw_attn_params;
+
+/* Bytes of workspace lbw_attention_fwd needs for these params (0 when single pass). */
+size_t lbw_attention_workspace_size(const lbw_attn_params* p);
+
+/* Chunk self-attention: softmax(scale * Q K^T) V over the windowed concatenation of the KV
+ * segments, bf16 MFMA, fp32 online softmax. */
+int lbw_attention_fwd(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Cross-attention to a short context (one segment of <= 4096 keys, typically 512), with the
+ * optional per-batch valid length p->k_lens. Single pass, no workspace. */
+int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream);
+
+/* fp8-e4m3 KV cache: K/V segments hold e4m3fn codes with per-(batch, head, 64-token block)
+ * fp32 scales (lbw_kv_quant_fp8's layout); Q stays bf16. */
+int lbw_attention_fwd_fp8kv(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* Log-sum-exp merge of n_parts partials (cte_merge): part_o[i] [B, H, Lq, D] fp32,
+ * part_m[i], part_l[i] [B, H, Lq] fp32 -> out bf16 [B, Lq, H, D] (strided). */
+int lbw_attn_merge(int32_t n_parts, const float* const* part_o, const float* const* part_m,
+                   const float* const* part_l, int32_t batch, int32_t heads, int32_t lq,
+                   int32_t head_dim, void* out, int64_t o_stride_b, int64_t o_stride_l,
+                   int64_t o_stride_h, void* stream);
+
+/* Fused q/k post-processing of one chunk (kernels/qk_post.py semantics, full-row RMSNorm):
+ *   y = x + b (fp32); r = rsqrt(sum(y^2)/C + eps); t = bf16(y*r) * gamma (fp32);
+ *   Wan 3-D RoPE on interleaved pairs (fp32); out = bf16(t_rot * out_scale).
+ * Tokens >= f*h*w pass the RoPE unrotated. The RoPE tables are the per-axis cos/sin rows,
+ * packed fp32: cos_t[f][s0], sin_t[f][s0], cos_h[h][s1], sin_h[h][s1], cos_w[w][s1],
+ * sin_w[w][s1] with s0 + 2*s1 = head_dim/2. Optionally copies v into v_out (the KV-cache
+ * commit of the new chunk's V). k_out/v_out may point into a KV cache slot. */
+typedef struct lbw_qk_norm_rope_params {
+  int32_t tokens, dim, heads;      /* L, C = heads * head_dim */
+  const void* q; int64_t q_stride; /* bf16 rows [L, C], row stride in elements */
+  const void* k; int64_t k_stride;
+  const void* bq; const void* bk;  /* bf16 [C] or NULL */
+  const void* wq; const void* wk;  /* bf16 [C] RMSNorm gamma */
+  float eps;
+  const float* rope;               /* packed per-axis tables (see above) */
+  int32_t grid_f, grid_h, grid_w, s0, s1;
+  void* q_out; int64_t q_out_stride;
+  void* k_out; int64_t k_out_stride;
+  float q_out_scale, k_out_scale;  /* 1.0 = none */
+  const void* v; int64_t v_stride; /* optional V copy (bf16 [L, C]); NULL = none */
+  void* v_out; int64_t v_out_stride;
+} lbw_qk_norm_rope_params;
+
+int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream);
+
+/* fp8-e4m3fn KV quantiser: x bf16 [B, L, H, D] (strided) -> codes uint8 [B, L, H, D]
+ * (contiguous) and scales fp32 [B, H, ceil(L / block)] (contiguous). Per (b, h, block):
+ * scale = amax / 448 (1 if amax == 0); code = rne_e4m3fn(x * (1 / scale)). */
+int lbw_kv_quant_fp8(const void* x, int32_t batch, int64_t len, int32_t heads,
+                     int32_t head_dim, int64_t s_b, int64_t s_l, int64_t s_h,
+                     uint8_t* codes, float* scales, int32_t block, void* stream);
+
+const char* lbw_last_error(void);
+int lbw_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LBW_ATTN_H */

@@ -1,0 +1,91 @@
+// Kernel-argument structs and launchers of the attention kernels (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lbw {
+
+constexpr int LBW_MAX_SEGS = 8;
+enum { kModeNormalized = 0, kModePartials = 1 };
+
+struct SegDesc {
+  const uint16_t* k;  // bf16 elements (or fp8 codes reinterpreted by the fp8 kernel)
+  const uint16_t* v;
+  int64_t start;      // first logical key of this segment
+  int64_t len;
+  int64_t ksb, ksl, ksh;
+  int64_t vsb, vsl, vsh;
+  const float* ks;    // fp8 scales [B, H, nblk]
+  const float* vs;
+  int64_t nblk;       // scale blocks per (b, h)
+};
+
+struct AttnKernelArgs {
+  const uint16_t* q;
+  int64_t qsb, qsl, qsh;
+  uint16_t* out;
+  int64_t osb, osl, osh;
+  int nseg;
+  SegDesc seg[LBW_MAX_SEGS];
+  int64_t total;      // keys in the concatenation
+  int64_t lo, hi;     // clamped window
+  const int32_t* k_lens;
+  float scale;        // softmax scale
+  float scale_log2;   // scale * log2(e)
+  int B, H, Lq;
+  int n_qtiles, splits;
+  int mode;
+  float* part_o;
+  float* part_m;
+  float* part_l;
+};
+
+struct MergeKernelArgs {
+  int n;
+  const float* o[16];
+  const float* m[16];
+  const float* l[16];
+  int B, H, Lq, D;
+  uint16_t* out;
+  int64_t osb, osl, osh;
+};
+
+int attn_lds_bytes();
+int attn_block_m();
+int attn_block_n();
+hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream);
+hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream);
+hipError_t launch_attn_merge(const MergeKernelArgs& a, hipStream_t stream);
+
+struct QkNormRopeArgs {
+  int L, C, H;
+  const uint16_t* q; int64_t qs;
+  const uint16_t* k; int64_t ks;
+  const uint16_t* bq; const uint16_t* bk;
+  const uint16_t* wq; const uint16_t* wk;
+  float eps, inv_c;
+  const float* rope;
+  int gf, gh, gw, s0, s1;
+  int ntab;            // floats of rope tables (0: no token is rotated)
+  uint16_t* qo; int64_t qos;
+  uint16_t* ko; int64_t kos;
+  float q_scale, k_scale;
+  const uint16_t* v; int64_t vs;
+  uint16_t* vo; int64_t vos;
+};
+hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, hipStream_t stream);
+int qk_norm_rope_max_table_floats();
+
+struct KvQuantArgs {
+  const uint16_t* x;
+  int B, H, D;
+  int64_t L, sb, sl, sh;
+  uint8_t* codes;
+  float* scales;
+  int block;
+  int64_t nblk;
+};
+hipError_t launch_kv_quant_fp8(const KvQuantArgs& a, hipStream_t stream);
+
+}  // namespace lbw

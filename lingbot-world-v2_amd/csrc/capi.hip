@@ -1,0 +1,341 @@
+// extern "C" entry points of liblbw_attn.so: argument validation, work decomposition and
+// kernel launches. No allocation and no device synchronisation happens here.
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+
+#include "lbw_attn.h"
+#include "attn_fwd.h"
+
+using namespace lbw;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(LBW_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool mult8(int64_t s) { return (s & 7) == 0; }
+
+int num_cus() {
+  static std::mutex mu;
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lk(mu);
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+struct Plan {
+  AttnKernelArgs a;
+  int splits;
+  size_t ws_bytes;
+};
+
+// Validates the params and fills the kernel arguments (everything but the output mode).
+int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
+  if (p == nullptr) return fail(LBW_ERR_INVALID, "params is NULL");
+  if (p->head_dim != 128)
+    return fail(LBW_ERR_UNSUPPORTED, "head_dim %d: only 128 is supported", p->head_dim);
+  if (p->batch < 1 || p->heads < 1 || p->lq < 0)
+    return fail(LBW_ERR_INVALID, "bad sizes batch=%d heads=%d lq=%d", p->batch, p->heads, p->lq);
+  if (p->n_segments < 1 || p->n_segments > LBW_MAX_KV_SEGMENTS)
+    return fail(LBW_ERR_INVALID, "n_segments %d not in [1, %d]", p->n_segments,
+                LBW_MAX_KV_SEGMENTS);
+  if (p->lq > 0 && (p->q == nullptr || !aligned16(p->q)))
+    return fail(LBW_ERR_INVALID, "q must be a 16-byte aligned device pointer");
+  if (!mult8(p->q_stride_b) || !mult8(p->q_stride_l) || !mult8(p->q_stride_h))
+    return fail(LBW_ERR_INVALID, "q strides must be multiples of 8 elements");
+  const bool partials = p->part_o != nullptr || p->part_m != nullptr || p->part_l != nullptr;
+  if (partials && (p->part_o == nullptr || p->part_m == nullptr || p->part_l == nullptr))
+    return fail(LBW_ERR_INVALID, "part_o, part_m and part_l must be given together");
+  if (partials && !aligned16(p->part_o)) return fail(LBW_ERR_INVALID, "part_o must be 16-byte aligned");
+  if (!partials) {
+    if (p->lq > 0 && (p->out == nullptr || (reinterpret_cast<uintptr_t>(p->out) & 7u) != 0))
+      return fail(LBW_ERR_INVALID, "out must be an 8-byte aligned device pointer");
+    if ((p->o_stride_b & 3) || (p->o_stride_l & 3) || (p->o_stride_h & 3))
+      return fail(LBW_ERR_INVALID, "out strides must be multiples of 4 elements");
+  }
+  if (partials && p->num_splits > 1)
+    return fail(LBW_ERR_INVALID, "partial outputs need num_splits <= 1");
+
+  AttnKernelArgs& a = plan->a;
+  memset(&a, 0, sizeof(a));
+  a.q = static_cast<const uint16_t*>(p->q);
+  a.qsb = p->q_stride_b; a.qsl = p->q_stride_l; a.qsh = p->q_stride_h;
+  a.out = static_cast<uint16_t*>(p->out);
+  a.osb = p->o_stride_b; a.osl = p->o_stride_l; a.osh = p->o_stride_h;
+  a.nseg = p->n_segments;
+  int64_t start = 0;
+  for (int i = 0; i < p->n_segments; ++i) {
+    const lbw_kv_segment& s = p->seg[i];
+    if (s.len < 0) return fail(LBW_ERR_INVALID, "segment %d: negative length", i);
+    if (s.len > 0) {
+      if (s.k == nullptr || s.v == nullptr || !aligned16(s.k) || !aligned16(s.v))
+        return fail(LBW_ERR_INVALID, "segment %d: k/v must be 16-byte aligned device pointers", i);
+      const int64_t el = fp8 ? 16 : 8;  // 16-byte granules in elements
+      if ((s.k_stride_b % el) || (s.k_stride_l % el) || (s.k_stride_h % el) ||
+          (s.v_stride_b % el) || (s.v_stride_l % el) || (s.v_stride_h % el))
+        return fail(LBW_ERR_INVALID, "segment %d: strides must be multiples of %lld elements", i,
+                    (long long)el);
+      if (fp8 && (s.k_scale == nullptr || s.v_scale == nullptr))
+        return fail(LBW_ERR_INVALID, "segment %d: fp8 scales missing", i);
+    }
+    SegDesc& d = a.seg[i];
+    d.k = static_cast<const uint16_t*>(s.k);
+    d.v = static_cast<const uint16_t*>(s.v);
+    d.start = start;
+    d.len = s.len;
+    d.ksb = s.k_stride_b; d.ksl = s.k_stride_l; d.ksh = s.k_stride_h;
+    d.vsb = s.v_stride_b; d.vsl = s.v_stride_l; d.vsh = s.v_stride_h;
+    d.ks = s.k_scale; d.vs = s.v_scale;
+    d.nblk = (s.len + LBW_FP8_BLOCK - 1) / LBW_FP8_BLOCK;
+    start += s.len;
+  }
+  a.total = start;
+  a.lo = p->kv_lo > 0 ? p->kv_lo : 0;
+  a.hi = (p->kv_hi < 0 || p->kv_hi > start) ? start : p->kv_hi;
+  if (a.hi < a.lo) a.hi = a.lo;
+  a.k_lens = p->k_lens;
+  const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf((float)p->head_dim);
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.B = p->batch; a.H = p->heads; a.Lq = p->lq;
+  const int bm = attn_block_m(), bn = attn_block_n();
+  a.n_qtiles = (p->lq + bm - 1) / bm;
+  a.part_o = p->part_o; a.part_m = p->part_m; a.part_l = p->part_l;
+  a.mode = partials ? kModePartials : kModeNormalized;
+
+  // KV splits: more workgroups when (q-tiles x heads x batch) leaves the last dispatch round
+  // of the CUs mostly empty. Each extra split costs one fp32 partial per query row.
+  int splits = 1;
+  if (!partials) {
+    if (p->num_splits > 0) {
+      splits = p->num_splits > 16 ? 16 : p->num_splits;
+    } else {
+      const int64_t base = (int64_t)a.n_qtiles * a.H * a.B;
+      const int64_t ntiles = (a.hi - a.lo + bn - 1) / bn;
+      const int cus = num_cus();
+      double best = 0.0;
+      for (int s = 1; s <= 8; ++s) {
+        if (s > 1 && ntiles / s < 8) break;
+        const int64_t n = base * s;
+        const int64_t rounds = (n + cus - 1) / cus;
+        const double eff = (double)n / (double)(rounds * cus);
+        if (eff > best * 1.03) { best = eff; splits = s; }
+      }
+    }
+  }
+  plan->splits = splits;
+  plan->ws_bytes = splits > 1 ? (size_t)splits * a.B * a.H * a.Lq * (p->head_dim + 2) * sizeof(float) : 0;
+  a.splits = splits;
+  return LBW_OK;
+}
+
+int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes, void* stream) {
+  Plan plan;
+  int rc = make_plan(p, fp8, &plan);
+  if (rc != LBW_OK) return rc;
+  if (p->lq == 0) return LBW_OK;
+  AttnKernelArgs& a = plan.a;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (plan.splits > 1) {
+    if (ws == nullptr || ws_bytes < plan.ws_bytes || !aligned16(ws))
+      return fail(LBW_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", plan.ws_bytes, ws_bytes);
+    const size_t rows = (size_t)plan.splits * a.B * a.H * a.Lq;
+    float* base = static_cast<float*>(ws);
+    a.part_o = base;
+    a.part_m = base + rows * p->head_dim;
+    a.part_l = a.part_m + rows;
+    a.mode = kModePartials;
+  }
+  hipError_t e = fp8 ? launch_attn_fwd_fp8(a, st) : launch_attn_fwd(a, st);
+  if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
+  if (plan.splits > 1) {
+    MergeKernelArgs m;
+    memset(&m, 0, sizeof(m));
+    m.n = plan.splits;
+    const size_t per = (size_t)a.B * a.H * a.Lq;
+    for (int s = 0; s < plan.splits; ++s) {
+      m.o[s] = a.part_o + s * per * p->head_dim;
+      m.m[s] = a.part_m + s * per;
+      m.l[s] = a.part_l + s * per;
+    }
+    m.B = a.B; m.H = a.H; m.Lq = a.Lq; m.D = p->head_dim;
+    m.out = static_cast<uint16_t*>(p->out);
+    m.osb = p->o_stride_b; m.osl = p->o_stride_l; m.osh = p->o_stride_h;
+    e = launch_attn_merge(m, st);
+    if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
+  }
+  return LBW_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* lbw_last_error(void) { return g_err.c_str(); }
+int lbw_abi_version(void) { return LBW_ABI_VERSION; }
+
+size_t lbw_attention_workspace_size(const lbw_attn_params* p) {
+  Plan plan;
+  if (make_plan(p, false, &plan) != LBW_OK) return 0;
+  return plan.ws_bytes;
+}
+
+int lbw_attention_fwd(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  return run_attention(p, false, workspace, workspace_bytes, stream);
+}
+
+int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream) {
+  if (p == nullptr) return fail(LBW_ERR_INVALID, "params is NULL");
+  if (p->n_segments != 1) return fail(LBW_ERR_INVALID, "cross-attention takes one KV segment");
+  if (p->seg[0].len > 4096)
+    return fail(LBW_ERR_INVALID, "cross-attention context of %lld keys exceeds 4096",
+                (long long)p->seg[0].len);
+  if (p->num_splits > 1) return fail(LBW_ERR_INVALID, "cross-attention is single pass");
+  lbw_attn_params q = *p;
+  q.num_splits = 1;
+  return run_attention(&q, false, nullptr, 0, stream);
+}
+
+int lbw_attention_fwd_fp8kv(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return run_attention(p, true, workspace, workspace_bytes, stream);
+}
+
+int lbw_attn_merge(int32_t n_parts, const float* const* part_o, const float* const* part_m,
+                   const float* const* part_l, int32_t batch, int32_t heads, int32_t lq,
+                   int32_t head_dim, void* out, int64_t o_stride_b, int64_t o_stride_l,
+                   int64_t o_stride_h, void* stream) {
+  if (n_parts < 1 || n_parts > 16) return fail(LBW_ERR_INVALID, "n_parts %d not in [1, 16]", n_parts);
+  if (head_dim != 128) return fail(LBW_ERR_UNSUPPORTED, "head_dim %d: only 128", head_dim);
+  if (batch < 1 || heads < 1 || lq < 0) return fail(LBW_ERR_INVALID, "bad sizes");
+  if (part_o == nullptr || part_m == nullptr || part_l == nullptr || out == nullptr)
+    return fail(LBW_ERR_INVALID, "NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(out) & 7u) || (o_stride_b & 3) || (o_stride_l & 3) ||
+      (o_stride_h & 3))
+    return fail(LBW_ERR_INVALID, "out must be 8-byte aligned with strides multiple of 4");
+  if (lq == 0) return LBW_OK;
+  MergeKernelArgs m;
+  memset(&m, 0, sizeof(m));
+  m.n = n_parts;
+  for (int i = 0; i < n_parts; ++i) {
+    if (part_o[i] == nullptr || part_m[i] == nullptr || part_l[i] == nullptr || !aligned16(part_o[i]))
+      return fail(LBW_ERR_INVALID, "partial %d: NULL or misaligned pointer", i);
+    m.o[i] = part_o[i];
+    m.m[i] = part_m[i];
+    m.l[i] = part_l[i];
+  }
+  m.B = batch; m.H = heads; m.Lq = lq; m.D = head_dim;
+  m.out = static_cast<uint16_t*>(out);
+  m.osb = o_stride_b; m.osl = o_stride_l; m.osh = o_stride_h;
+  hipError_t e = launch_attn_merge(m, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
+  return LBW_OK;
+}
+
+int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream) {
+  if (p == nullptr) return fail(LBW_ERR_INVALID, "params is NULL");
+  if (p->tokens < 0 || p->heads < 1 || p->dim < 8 || p->dim % p->heads != 0)
+    return fail(LBW_ERR_INVALID, "bad sizes tokens=%d dim=%d heads=%d", p->tokens, p->dim, p->heads);
+  const int D = p->dim / p->heads;
+  if (D % 8 != 0 || p->dim % 8 != 0 || p->dim > 8192)
+    return fail(LBW_ERR_UNSUPPORTED, "dim %d / head_dim %d: need multiples of 8, dim <= 8192",
+                p->dim, D);
+  if (p->s0 < 0 || p->s1 < 0 || p->s0 + 2 * p->s1 != D / 2)
+    return fail(LBW_ERR_INVALID, "rope split s0=%d s1=%d does not cover head_dim/2=%d", p->s0,
+                p->s1, D / 2);
+  if (p->grid_f < 0 || p->grid_h < 0 || p->grid_w < 0)
+    return fail(LBW_ERR_INVALID, "negative grid");
+  const int64_t gt = (int64_t)p->grid_f * p->grid_h * p->grid_w;
+  if (gt > 0 && (p->grid_h == 0 || p->grid_w == 0)) return fail(LBW_ERR_INVALID, "bad grid");
+  const int64_t ntab = 2 * ((int64_t)p->grid_f * p->s0 + (int64_t)p->grid_h * p->s1 +
+                            (int64_t)p->grid_w * p->s1);
+  if (ntab > qk_norm_rope_max_table_floats())
+    return fail(LBW_ERR_UNSUPPORTED, "rope tables of %lld floats exceed %d", (long long)ntab,
+                qk_norm_rope_max_table_floats());
+  if (gt > 0 && p->rope == nullptr) return fail(LBW_ERR_INVALID, "rope tables missing");
+  if (p->tokens == 0) return LBW_OK;
+  const void* ptrs[] = {p->q, p->k, p->wq, p->wk, p->q_out, p->k_out};
+  for (const void* q : ptrs)
+    if (q == nullptr || !aligned16(q)) return fail(LBW_ERR_INVALID, "q/k/gamma/outputs must be 16-byte aligned");
+  if ((p->bq && !aligned16(p->bq)) || (p->bk && !aligned16(p->bk)))
+    return fail(LBW_ERR_INVALID, "bias must be 16-byte aligned");
+  if (!mult8(p->q_stride) || !mult8(p->k_stride) || !mult8(p->q_out_stride) || !mult8(p->k_out_stride))
+    return fail(LBW_ERR_INVALID, "row strides must be multiples of 8 elements");
+  if (p->v != nullptr && (p->v_out == nullptr || !aligned16(p->v) || !aligned16(p->v_out) ||
+                          !mult8(p->v_stride) || !mult8(p->v_out_stride)))
+    return fail(LBW_ERR_INVALID, "v copy: aligned v and v_out with 8-element strides needed");
+  QkNormRopeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.L = p->tokens; a.C = p->dim; a.H = p->heads;
+  a.q = static_cast<const uint16_t*>(p->q); a.qs = p->q_stride;
+  a.k = static_cast<const uint16_t*>(p->k); a.ks = p->k_stride;
+  a.bq = static_cast<const uint16_t*>(p->bq); a.bk = static_cast<const uint16_t*>(p->bk);
+  a.wq = static_cast<const uint16_t*>(p->wq); a.wk = static_cast<const uint16_t*>(p->wk);
+  a.eps = p->eps;
+  a.inv_c = 1.0f / (float)p->dim;
+  a.rope = p->rope;
+  a.gf = p->grid_f; a.gh = p->grid_h; a.gw = p->grid_w; a.s0 = p->s0; a.s1 = p->s1;
+  a.ntab = (int)ntab;
+  if (gt == 0) { a.gf = 0; a.gh = 1; a.gw = 1; a.ntab = 0; }
+  a.qo = static_cast<uint16_t*>(p->q_out); a.qos = p->q_out_stride;
+  a.ko = static_cast<uint16_t*>(p->k_out); a.kos = p->k_out_stride;
+  a.q_scale = p->q_out_scale; a.k_scale = p->k_out_scale;
+  a.v = static_cast<const uint16_t*>(p->v); a.vs = p->v_stride;
+  a.vo = static_cast<uint16_t*>(p->v_out); a.vos = p->v_out_stride;
+  hipError_t e = launch_qk_norm_rope(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "qk_norm_rope launch");
+  return LBW_OK;
+}
+
+int lbw_kv_quant_fp8(const void* x, int32_t batch, int64_t len, int32_t heads, int32_t head_dim,
+                     int64_t s_b, int64_t s_l, int64_t s_h, uint8_t* codes, float* scales,
+                     int32_t block, void* stream) {
+  if (head_dim != 128) return fail(LBW_ERR_UNSUPPORTED, "head_dim %d: only 128", head_dim);
+  if (block != LBW_FP8_BLOCK) return fail(LBW_ERR_UNSUPPORTED, "block %d: only %d", block, LBW_FP8_BLOCK);
+  if (batch < 1 || heads < 1 || len < 0) return fail(LBW_ERR_INVALID, "bad sizes");
+  if (len == 0) return LBW_OK;
+  if (x == nullptr || codes == nullptr || scales == nullptr || !aligned16(x) || !aligned16(codes))
+    return fail(LBW_ERR_INVALID, "x/codes must be 16-byte aligned device pointers, scales non-NULL");
+  if (!mult8(s_b) || !mult8(s_l) || !mult8(s_h))
+    return fail(LBW_ERR_INVALID, "x strides must be multiples of 8 elements");
+  KvQuantArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.B = batch; a.H = heads; a.D = head_dim; a.L = len;
+  a.sb = s_b; a.sl = s_l; a.sh = s_h;
+  a.codes = codes; a.scales = scales; a.block = block;
+  a.nblk = (len + block - 1) / block;
+  hipError_t e = launch_kv_quant_fp8(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "kv_quant_fp8 launch");
+  return LBW_OK;
+}
+
+}  // extern "C"

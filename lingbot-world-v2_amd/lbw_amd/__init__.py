@@ -1,0 +1,20 @@
+"""lbw_amd -- MI355X (gfx950) causal-chunk attention path of LingBot-World.
+
+Host-side mirror of the reference's attention interface (wan/modules/attention.py,
+kernels/qk_post.py, wan/modules/chunked_kv_cache.py) over the C ABI of liblbw_attn.so
+(include/lbw_attn.h). Importing is cheap; the HIP library loads on first use and raises
+when it is missing.
+"""
+from .attention import (attention, attention_merge, attention_partial, attention_segments,
+                        cross_attention, exact_attention, exact_attention_chunks,
+                        flash_attention)
+from .fp8 import Fp8KV, attention_fp8kv, quantize_kv_fp8
+from .qk_post import qk_norm_rope, qk_norm_rope_
+from .rope import RopeTables, causal_rope_tables, rope_params, wan_rope_freqs
+
+__all__ = [
+    "attention", "flash_attention", "exact_attention", "exact_attention_chunks",
+    "cross_attention", "attention_partial", "attention_merge", "attention_segments",
+    "qk_norm_rope", "qk_norm_rope_", "RopeTables", "causal_rope_tables", "rope_params",
+    "wan_rope_freqs", "Fp8KV", "quantize_kv_fp8", "attention_fp8kv",
+]

@@ -1,0 +1,136 @@
+"""ctypes binding of liblbw_attn.so (the C ABI declared in include/lbw_attn.h).
+
+The library is built in-tree (``make -C lingbot-world-v2_amd/csrc``) and loaded from this
+directory. There is no fallback: if the library is missing or a call fails, a RuntimeError
+says so.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liblbw_attn.so")
+
+MAX_KV_SEGMENTS = 8
+FP8_BLOCK = 64
+ABI_VERSION = 1
+
+LBW_OK = 0
+_ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "HIP error", 4: "workspace"}
+
+
+class KvSegment(ctypes.Structure):
+    _fields_ = [
+        ("k", ctypes.c_void_p), ("v", ctypes.c_void_p), ("len", ctypes.c_int64),
+        ("k_stride_b", ctypes.c_int64), ("k_stride_l", ctypes.c_int64), ("k_stride_h", ctypes.c_int64),
+        ("v_stride_b", ctypes.c_int64), ("v_stride_l", ctypes.c_int64), ("v_stride_h", ctypes.c_int64),
+        ("k_scale", ctypes.c_void_p), ("v_scale", ctypes.c_void_p),
+    ]
+
+
+class AttnParams(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int32), ("heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+        ("lq", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("q_stride_b", ctypes.c_int64), ("q_stride_l", ctypes.c_int64), ("q_stride_h", ctypes.c_int64),
+        ("out", ctypes.c_void_p),
+        ("o_stride_b", ctypes.c_int64), ("o_stride_l", ctypes.c_int64), ("o_stride_h", ctypes.c_int64),
+        ("n_segments", ctypes.c_int32),
+        ("seg", KvSegment * MAX_KV_SEGMENTS),
+        ("kv_lo", ctypes.c_int64), ("kv_hi", ctypes.c_int64),
+        ("k_lens", ctypes.c_void_p),
+        ("softmax_scale", ctypes.c_float),
+        ("num_splits", ctypes.c_int32),
+        ("part_o", ctypes.c_void_p), ("part_m", ctypes.c_void_p), ("part_l", ctypes.c_void_p),
+    ]
+
+
+class QkNormRopeParams(ctypes.Structure):
+    _fields_ = [
+        ("tokens", ctypes.c_int32), ("dim", ctypes.c_int32), ("heads", ctypes.c_int32),
+        ("q", ctypes.c_void_p), ("q_stride", ctypes.c_int64),
+        ("k", ctypes.c_void_p), ("k_stride", ctypes.c_int64),
+        ("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p),
+        ("wq", ctypes.c_void_p), ("wk", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("rope", ctypes.c_void_p),
+        ("grid_f", ctypes.c_int32), ("grid_h", ctypes.c_int32), ("grid_w", ctypes.c_int32),
+        ("s0", ctypes.c_int32), ("s1", ctypes.c_int32),
+        ("q_out", ctypes.c_void_p), ("q_out_stride", ctypes.c_int64),
+        ("k_out", ctypes.c_void_p), ("k_out_stride", ctypes.c_int64),
+        ("q_out_scale", ctypes.c_float), ("k_out_scale", ctypes.c_float),
+        ("v", ctypes.c_void_p), ("v_stride", ctypes.c_int64),
+        ("v_out", ctypes.c_void_p), ("v_out_stride", ctypes.c_int64),
+    ]
+
+
+EXPORTS = (
+    "lbw_attention_workspace_size", "lbw_attention_fwd", "lbw_cross_attention_fwd",
+    "lbw_attention_fwd_fp8kv", "lbw_attn_merge", "lbw_qk_norm_rope", "lbw_kv_quant_fp8",
+    "lbw_last_error", "lbw_abi_version",
+)
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _declare(lib):
+    P = ctypes.POINTER
+    vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.lbw_attention_workspace_size.argtypes = [P(AttnParams)]
+    lib.lbw_attention_workspace_size.restype = ctypes.c_size_t
+    lib.lbw_attention_fwd.argtypes = [P(AttnParams), vp, ctypes.c_size_t, vp]
+    lib.lbw_attention_fwd.restype = ctypes.c_int
+    lib.lbw_cross_attention_fwd.argtypes = [P(AttnParams), vp]
+    lib.lbw_cross_attention_fwd.restype = ctypes.c_int
+    lib.lbw_attention_fwd_fp8kv.argtypes = [P(AttnParams), vp, ctypes.c_size_t, vp]
+    lib.lbw_attention_fwd_fp8kv.restype = ctypes.c_int
+    lib.lbw_attn_merge.argtypes = [i32, P(vp), P(vp), P(vp), i32, i32, i32, i32, vp, i64, i64,
+                                   i64, vp]
+    lib.lbw_attn_merge.restype = ctypes.c_int
+    lib.lbw_qk_norm_rope.argtypes = [P(QkNormRopeParams), vp]
+    lib.lbw_qk_norm_rope.restype = ctypes.c_int
+    lib.lbw_kv_quant_fp8.argtypes = [vp, i32, i64, i32, i32, i64, i64, i64, vp, vp, i32, vp]
+    lib.lbw_kv_quant_fp8.restype = ctypes.c_int
+    lib.lbw_last_error.argtypes = []
+    lib.lbw_last_error.restype = ctypes.c_char_p
+    lib.lbw_abi_version.argtypes = []
+    lib.lbw_abi_version.restype = ctypes.c_int
+
+
+def load():
+    """Load (once) and return the library handle. Raises RuntimeError when it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `make -C lingbot-world-v2_amd/csrc` "
+                "(or __graft_entry__.build()). The attention path has no CPU fallback.")
+        # torch first: its libamdhip64 (same soname) then serves the library's HIP calls,
+        # so there is exactly one HIP runtime in the process.
+        import torch  # noqa: F401
+        lib = ctypes.CDLL(LIB_PATH)
+        _declare(lib)
+        if lib.lbw_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"liblbw_attn ABI {lib.lbw_abi_version()} != {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str):
+    if rc != LBW_OK:
+        msg = load().lbw_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({_ERR_NAMES.get(rc, rc)}): {msg}")
+
+
+def stream_ptr(device=None) -> int:
+    """The current torch stream on `device` as a hipStream_t address."""
+    import torch
+    return torch.cuda.current_stream(device).cuda_stream

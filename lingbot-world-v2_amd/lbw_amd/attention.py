@@ -1,0 +1,266 @@
+"""Drop-in attention entry points backed by the gfx950 kernels of liblbw_attn.so.
+
+Mirrors wan/modules/attention.py: ``attention()`` keeps the reference signature
+(attention.py:1082-1100) and its layout contract (q ``[B, Lq, N, D]``, k/v ``[B, Lk, N, D]``
+-> ``[B, Lq, N, D]``), ``flash_attention`` is its alias (attention.py:1146),
+``exact_attention`` / ``exact_attention_chunks`` take the chunked cache's chunk lists
+without concatenating them (attention.py:1048-1079), and ``attention_partial`` /
+``attention_merge`` carry the unnormalised (O, row max, row sum) contract of
+``cte_partial`` / ``cte_merge`` (attention.py:617-645, 963-990).
+
+Every call runs on the tensors' device on torch's current stream and raises when the
+library is missing or rejects the arguments: there is no CPU or SDPA fallback.
+"""
+from __future__ import annotations
+
+import math
+import warnings
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+__all__ = ["attention", "flash_attention", "exact_attention", "exact_attention_chunks",
+           "cross_attention", "attention_partial", "attention_merge", "attention_segments",
+           "window_from_mask"]
+
+_ws_cache: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A per-device scratch buffer for split-KV partials, grown on demand (torch allocator)."""
+    key = (device.type, device.index)
+    buf = _ws_cache.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _ws_cache[key] = buf
+    return buf
+
+
+def _as_bf16(t: torch.Tensor) -> torch.Tensor:
+    t = t if t.dtype == torch.bfloat16 else t.to(torch.bfloat16)
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    return t
+
+
+def _check_4d(name, t, device):
+    if t.dim() != 4:
+        raise ValueError(f"{name} must be [B, L, N, D], got shape {tuple(t.shape)}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, q on {device}")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a GPU tensor (the path has no CPU implementation)")
+
+
+def _fill_segment(seg: _lib.KvSegment, k: torch.Tensor, v: torch.Tensor, k_scale=None,
+                  v_scale=None):
+    seg.k = k.data_ptr()
+    seg.v = v.data_ptr()
+    seg.len = k.shape[1]
+    seg.k_stride_b, seg.k_stride_l, seg.k_stride_h = k.stride(0), k.stride(1), k.stride(2)
+    seg.v_stride_b, seg.v_stride_l, seg.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
+    seg.k_scale = k_scale.data_ptr() if k_scale is not None else None
+    seg.v_scale = v_scale.data_ptr() if v_scale is not None else None
+
+
+def _params(q, out, segments, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, parts=None):
+    p = _lib.AttnParams()
+    B, Lq, H, D = q.shape
+    p.batch, p.heads, p.head_dim, p.lq = B, H, D, Lq
+    p.q = q.data_ptr()
+    p.q_stride_b, p.q_stride_l, p.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    if out is not None:
+        p.out = out.data_ptr()
+        p.o_stride_b, p.o_stride_l, p.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
+    if not 1 <= len(segments) <= _lib.MAX_KV_SEGMENTS:
+        raise ValueError(f"{len(segments)} KV segments: 1..{_lib.MAX_KV_SEGMENTS} supported")
+    p.n_segments = len(segments)
+    for i, sg in enumerate(segments):
+        _fill_segment(p.seg[i], *sg)
+    p.kv_lo = 0 if kv_lo is None else int(kv_lo)
+    p.kv_hi = -1 if kv_hi is None else int(kv_hi)
+    p.k_lens = k_lens.data_ptr() if k_lens is not None else None
+    p.softmax_scale = 0.0 if softmax_scale is None else float(softmax_scale)
+    p.num_splits = int(num_splits)
+    if parts is not None:
+        p.part_o, p.part_m, p.part_l = (t.data_ptr() for t in parts)
+    return p
+
+
+def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi=None,
+                       k_lens: torch.Tensor | None = None, softmax_scale=None,
+                       num_splits: int = 0, out: torch.Tensor | None = None,
+                       cross: bool = False) -> torch.Tensor:
+    """softmax(scale Q K^T) V over the windowed concatenation of KV ``segments``.
+
+    q ``[B, Lq, N, 128]``; each segment is ``(k, v)`` with k/v ``[B, L_i, N, 128]`` (strided
+    views are fine as long as the head dim is contiguous); the window ``[kv_lo, kv_hi)``
+    indexes the concatenation. ``k_lens`` (int32 ``[B]`` on the device) limits each batch's
+    keys. Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given)."""
+    lib = _lib.load()
+    device = q.device
+    _check_4d("q", q, device)
+    q = _as_bf16(q)
+    segs = []
+    for k, v in segments:
+        _check_4d("k", k, device)
+        _check_4d("v", v, device)
+        segs.append((_as_bf16(k), _as_bf16(v)))
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.bfloat16, device=device)
+    if k_lens is not None:
+        k_lens = k_lens.to(device=device, dtype=torch.int32).contiguous()
+    p = _params(q, out, segs, kv_lo, kv_hi, k_lens, softmax_scale, 1 if cross else num_splits)
+    stream = _lib.stream_ptr(device)
+    with torch.cuda.device(device):
+        if cross:
+            _lib.check(lib.lbw_cross_attention_fwd(ctypes_ref(p), stream), "lbw_cross_attention_fwd")
+        else:
+            ws_bytes = lib.lbw_attention_workspace_size(ctypes_ref(p))
+            ws = _workspace(device, ws_bytes) if ws_bytes else None
+            _lib.check(lib.lbw_attention_fwd(ctypes_ref(p), ws.data_ptr() if ws is not None else None,
+                                             ws_bytes, stream), "lbw_attention_fwd")
+    return out
+
+
+def ctypes_ref(p):
+    import ctypes
+    return ctypes.byref(p)
+
+
+def window_from_mask(attn_mask: torch.Tensor, lk: int):
+    """(lo, hi) of a KV-window mask as model_fast.py:2538-2545 builds it (bool, True =
+    attend, broadcast over batch, heads and queries). Raises for any other mask."""
+    if attn_mask.dtype != torch.bool:
+        raise ValueError("only boolean KV-window masks are supported")
+    m = attn_mask.reshape(-1, attn_mask.shape[-1])
+    if attn_mask.shape[-1] != lk or not bool(torch.all(m == m[:1])):
+        raise ValueError("attn_mask must be a [.., Lk] KV window shared by every query")
+    idx = torch.nonzero(m[0]).flatten()
+    if idx.numel() == 0:
+        return 0, 0
+    lo, hi = int(idx[0]), int(idx[-1]) + 1
+    if idx.numel() != hi - lo:
+        raise ValueError("attn_mask is not a contiguous KV window")
+    return lo, hi
+
+
+def _scalar(x):
+    return int(x.item()) if torch.is_tensor(x) else int(x)
+
+
+def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=None,
+              q_scale=None, causal=False, window_size=(-1, -1), deterministic=False,
+              dtype=torch.bfloat16, fa_version=None, attn_mask=None, is_cross_attn=False,
+              kv_lo=None, kv_hi=None):
+    """attention.py:1082-1143 with the reference's signature and layout.
+
+    Differences from the reference's SDPA fallback, all loud: ``causal=True``,
+    ``dropout_p > 0`` and masks that are not a KV window raise. ``kv_lo``/``kv_hi`` (ints
+    or 0-d tensors) take precedence over ``attn_mask`` (they carry the same window,
+    model_fast.py:2546-2550). ``q_lens``/``k_lens`` are ignored with the reference's
+    warning (attention.py:1128-1132); masked cross-attention is ``cross_attention``.
+    Output: ``[B, Lq, N, D]`` in ``dtype`` (bf16 by default)."""
+    if causal:
+        raise NotImplementedError("causal masking is not part of this path (the chunked "
+                                  "cache carries causality; attention.py:360-365)")
+    if dropout_p:
+        raise NotImplementedError("dropout is not supported")
+    if window_size not in ((-1, -1), [-1, -1]):
+        raise NotImplementedError("local window_size is not supported")
+    if q_lens is not None or k_lens is not None:
+        warnings.warn('Padding mask is disabled when using scaled_dot_product_attention. '
+                      'It can have a significant impact on performance.')
+    if q_scale is not None:
+        q = q * q_scale
+    lo = _scalar(kv_lo) if kv_lo is not None else None
+    hi = _scalar(kv_hi) if kv_hi is not None else None
+    if attn_mask is not None and lo is None and hi is None:
+        lo, hi = window_from_mask(attn_mask, k.shape[1])
+    out = attention_segments(q, [(k, v)], kv_lo=lo, kv_hi=hi, softmax_scale=softmax_scale,
+                             cross=bool(is_cross_attn) and k.shape[1] <= 4096)
+    return out if dtype == torch.bfloat16 else out.to(dtype)
+
+
+flash_attention = attention
+
+
+def exact_attention(q, k, v, dtype=torch.bfloat16):
+    """attention.py:1061-1079: exact attention, streamed (no score matrix)."""
+    return attention(q, k, v, dtype=dtype)
+
+
+def exact_attention_chunks(q, k_chunks, v_chunks, dtype=torch.bfloat16):
+    """attention.py:1048-1058: attention over the concatenation of KV chunks, read in
+    place as segments (no torch.cat, no padding copy). Chunks are ``[B, L_c, N, D]``."""
+    if len(k_chunks) != len(v_chunks):
+        raise ValueError("k_chunks and v_chunks differ in length")
+    out = attention_segments(q, list(zip(k_chunks, v_chunks)))
+    return out if dtype == torch.bfloat16 else out.to(dtype)
+
+
+def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16):
+    """Cross-attention to a short context (kernels/cross_attention.py:17 semantics), with the
+    optional per-batch valid length ``k_lens`` masked (the reference attends all rows;
+    ``k_lens=None`` reproduces that)."""
+    out = attention_segments(q, [(k, v)], k_lens=k_lens, cross=True)
+    return out if dtype == torch.bfloat16 else out.to(dtype)
+
+
+def attention_partial(q, segments, *, kv_lo=None, kv_hi=None, softmax_scale=None):
+    """cte_partial (attention.py:617-645): unnormalised attention over ``segments``.
+
+    Returns ``(O [B, N, Lq, D] fp32, m [B, N, Lq] fp32, l [B, N, Lq] fp32)`` with
+    O = exp(s - m) V, m the row max of the scaled scores and l = sum exp(s - m)
+    (m = -inf, l = 0 for rows with no keys)."""
+    lib = _lib.load()
+    device = q.device
+    _check_4d("q", q, device)
+    q = _as_bf16(q)
+    segs = [(_as_bf16(k), _as_bf16(v)) for k, v in segments]
+    B, Lq, H, D = q.shape
+    po = torch.empty(B, H, Lq, D, dtype=torch.float32, device=device)
+    pm = torch.empty(B, H, Lq, dtype=torch.float32, device=device)
+    pl = torch.empty(B, H, Lq, dtype=torch.float32, device=device)
+    p = _params(q, None, segs, kv_lo, kv_hi, None, softmax_scale, 1, parts=(po, pm, pl))
+    with torch.cuda.device(device):
+        _lib.check(lib.lbw_attention_fwd(ctypes_ref(p), None, 0, _lib.stream_ptr(device)),
+                   "lbw_attention_fwd(partials)")
+    return po, pm, pl
+
+
+def attention_merge(parts, out: torch.Tensor | None = None) -> torch.Tensor:
+    """cte_merge (attention.py:963-990): out = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c
+    over partials ``(O [B, N, Lq, D], m [B, N, Lq], l [B, N, Lq])`` -> bf16 ``[B, Lq, N, D]``."""
+    import ctypes
+    lib = _lib.load()
+    if not 1 <= len(parts) <= 16:
+        raise ValueError("1..16 partials")
+    po0 = parts[0][0]
+    B, H, Lq, D = po0.shape
+    device = po0.device
+    for o, m, l in parts:
+        if o.shape != po0.shape or m.shape != (B, H, Lq) or l.shape != (B, H, Lq):
+            raise ValueError("partials differ in shape")
+        if not (o.is_contiguous() and m.is_contiguous() and l.is_contiguous()):
+            raise ValueError("partials must be contiguous")
+        if o.dtype != torch.float32 or m.dtype != torch.float32 or l.dtype != torch.float32:
+            raise ValueError("partials must be float32")
+    if out is None:
+        out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=device)
+    n = len(parts)
+    arr = ctypes.c_void_p * n
+    po = arr(*[p[0].data_ptr() for p in parts])
+    pm = arr(*[p[1].data_ptr() for p in parts])
+    pl = arr(*[p[2].data_ptr() for p in parts])
+    with torch.cuda.device(device):
+        _lib.check(lib.lbw_attn_merge(n, po, pm, pl, B, H, Lq, D, out.data_ptr(), out.stride(0),
+                                      out.stride(1), out.stride(2), _lib.stream_ptr(device)),
+                   "lbw_attn_merge")
+    return out
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)

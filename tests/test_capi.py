@@ -1,0 +1,80 @@
+"""CPU checks of the C ABI: the in-tree library loads, exports every function that
+include/lbw_attn.h declares, and the ctypes structs match the header's field lists.
+No compute call is made (no GPU here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lbw_attn.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lbw_[a-z0-9_]+)\s*\(", text)))
+
+
+def _lib_path():
+    from lbw_amd import _lib
+    return _lib.LIB_PATH
+
+
+def test_header_declares_expected_entry_points():
+    from lbw_amd import _lib
+    assert _header_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    path = _lib_path()
+    if not os.path.exists(path):
+        pytest.fail(f"{path} not built: run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+    lib.lbw_abi_version.restype = ctypes.c_int
+    assert lib.lbw_abi_version() == 1
+
+
+def _header_struct_fields(name):
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    m = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S)
+    assert m, name
+    fields = []
+    for decl in m.group(1).split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        decl = re.sub(r"\[[^\]]*\]", "", decl)
+        names = decl.split(None, 1)[1] if " " in decl else decl
+        for n in names.split(","):
+            fields.append(n.replace("*", "").strip().split()[-1])
+    return fields
+
+
+@pytest.mark.parametrize("cname,pyname", [("lbw_kv_segment", "KvSegment"),
+                                          ("lbw_attn_params", "AttnParams"),
+                                          ("lbw_qk_norm_rope_params", "QkNormRopeParams")])
+def test_ctypes_structs_match_header(cname, pyname):
+    from lbw_amd import _lib
+    py = [f[0] for f in getattr(_lib, pyname)._fields_]
+    assert py == _header_struct_fields(cname)
+
+
+def test_entry_points_reject_bad_arguments_without_gpu():
+    """Validation runs before any HIP call: bad params return LBW_ERR_* with a message."""
+    from lbw_amd import _lib
+    lib = ctypes.CDLL(_lib_path())
+    _lib._declare(lib)
+    p = _lib.AttnParams()
+    p.batch, p.heads, p.head_dim, p.lq = 1, 1, 64, 4
+    assert lib.lbw_attention_fwd(ctypes.byref(p), None, 0, None) == 2
+    assert b"head_dim" in lib.lbw_last_error()
+    p.head_dim = 128
+    p.n_segments = 0
+    assert lib.lbw_attention_fwd(ctypes.byref(p), None, 0, None) == 1
+    assert lib.lbw_attention_workspace_size(ctypes.byref(p)) == 0
+    assert lib.lbw_kv_quant_fp8(None, 1, 10, 1, 128, 0, 0, 0, None, None, 32, None) == 2

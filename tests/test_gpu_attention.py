@@ -1,0 +1,178 @@
+"""GPU parity of the chunk flash-attention kernel (lbw_attention_fwd / lbw_cross_attention_fwd)
+against the fp32 CPU oracle, through the product wrappers over the C ABI."""
+import math
+
+import pytest
+import torch
+
+import oracle as O
+from parity import assert_parity, metrics
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _rand(shape, g, scale=1.0):
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _gains(H):
+    base = torch.tensor([0.25, 0.5, 1.0, 2.0, 4.0, 8.0, 16.0, 1.0])
+    return base[torch.arange(H) % len(base)]
+
+
+def _case(B, Lq, H, seg_lens, seed, gain=True):
+    g = torch.Generator().manual_seed(seed)
+    q = _rand((B, Lq, H, 128), g)
+    if gain:
+        q = (q.float() * _gains(H).view(1, 1, H, 1)).to(torch.bfloat16)
+    ks = [_rand((B, L, H, 128), g) for L in seg_lens]
+    vs = [_rand((B, L, H, 128), g) for L in seg_lens]
+    return q, ks, vs
+
+
+@pytest.mark.parametrize("B,Lq,H,seg_lens,window", [
+    (1, 300, 2, [1000], None),
+    (1, 37, 3, [64], None),
+    (1, 1, 1, [1], None),
+    (1, 257, 2, [65], None),
+    (2, 129, 2, [100, 37, 200, 5], (50, 300)),
+    (1, 512, 4, [4096, 1560], (1000, 5656)),
+    (1, 96, 2, [7, 0, 130], None),
+])
+def test_attention_matches_oracle(lib, B, Lq, H, seg_lens, window):
+    from lbw_amd import attention_segments
+    q, ks, vs = _case(B, Lq, H, seg_lens, seed=Lq + H)
+    lo, hi = (None, None) if window is None else window
+    out = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV)) for k, v in zip(ks, vs)],
+                             kv_lo=lo, kv_hi=hi)
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1), kv_lo=lo, kv_hi=hi)
+    print(f"case B={B} Lq={Lq} H={H} segs={seg_lens} window={window}", metrics(out, ref))
+    assert_parity(out, ref)
+
+
+def test_attention_dropin_signature_and_mask(lib):
+    from lbw_amd import attention, flash_attention
+    q, ks, vs = _case(1, 200, 2, [777], seed=5)
+    k, v = ks[0], vs[0]
+    mask = O.window_mask(777, 100, 650)
+    ref = O.sdpa_ref(q, k, v, attn_mask=mask)
+    out = attention(q.to(DEV), k.to(DEV), v.to(DEV), attn_mask=mask.to(DEV))
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    assert_parity(out, ref, "attn_mask")
+    out2 = flash_attention(q.to(DEV), k.to(DEV), v.to(DEV), kv_lo=torch.tensor(100),
+                           kv_hi=torch.tensor(650))
+    assert torch.equal(out, out2)
+    with pytest.raises(NotImplementedError):
+        attention(q.to(DEV), k.to(DEV), v.to(DEV), causal=True)
+
+
+def test_strided_views_from_fused_qkv(lib):
+    from lbw_amd import attention_segments
+    g = torch.Generator().manual_seed(11)
+    B, L, H = 2, 333, 3
+    qkv = _rand((B, L, 3, H, 128), g)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    out = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV))])
+    d = qkv.to(DEV)
+    out_v = attention_segments(d[:, :, 0], [(d[:, :, 1], d[:, :, 2])])
+    ref = O.attention_ref(q, k, v)
+    assert_parity(out_v, ref, "strided")
+    assert torch.equal(out, out_v)
+
+
+def test_empty_window_gives_zero(lib):
+    from lbw_amd import attention_segments
+    q, ks, vs = _case(1, 70, 2, [300], seed=3)
+    out = attention_segments(q.to(DEV), [(ks[0].to(DEV), vs[0].to(DEV))], kv_lo=120, kv_hi=120)
+    assert torch.all(out == 0)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 7])
+def test_split_kv_merge_matches_single_pass(lib, splits):
+    from lbw_amd import attention_segments
+    q, ks, vs = _case(1, 300, 2, [3000, 600], seed=splits)
+    segs = [(k.to(DEV), v.to(DEV)) for k, v in zip(ks, vs)]
+    one = attention_segments(q.to(DEV), segs, num_splits=1)
+    many = attention_segments(q.to(DEV), segs, num_splits=splits)
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1))
+    assert_parity(one, ref, "single")
+    assert_parity(many, ref, f"splits={splits}")
+    assert (one.float() - many.float()).abs().max() < 4e-3
+
+
+def test_partials_match_oracle_and_merge(lib):
+    from lbw_amd import attention_merge, attention_partial
+    q, ks, vs = _case(1, 150, 2, [500, 260], seed=21)
+    parts_gpu = [attention_partial(q.to(DEV), [(k.to(DEV), v.to(DEV))]) for k, v in zip(ks, vs)]
+    for (po, pm, pl), k, v in zip(parts_gpu, ks, vs):
+        _, (ro, rm, rl) = O.attention_ref(q, k, v, return_partials=True)
+        assert torch.allclose(pm.cpu(), rm, rtol=1e-5, atol=1e-4)
+        assert torch.allclose(pl.cpu(), rl, rtol=5e-3, atol=1e-3)
+        assert (po.cpu() - ro).abs().max() <= 1e-2 * max(1.0, float(rl.max()))
+    merged = attention_merge(parts_gpu)
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1))
+    assert_parity(merged, ref, "merge")
+
+
+def test_cross_attention_masked_and_unmasked(lib):
+    from lbw_amd import attention, cross_attention
+    g = torch.Generator().manual_seed(7)
+    B, Lq, H = 2, 333, 4
+    q = _rand((B, Lq, H, 128), g, 2.0)
+    k = _rand((B, 512, H, 128), g)
+    v = _rand((B, 512, H, 128), g)
+    k_lens = torch.tensor([300, 512], dtype=torch.int32)
+    out = cross_attention(q.to(DEV), k.to(DEV), v.to(DEV), k_lens=k_lens.to(DEV))
+    ref = O.attention_ref(q, k, v, k_lens=k_lens)
+    assert_parity(out, ref, "masked")
+    out_u = attention(q.to(DEV), k.to(DEV), v.to(DEV), is_cross_attn=True)
+    assert_parity(out_u, O.attention_ref(q, k, v), "unmasked")
+
+
+def test_deterministic_bitwise(lib):
+    from lbw_amd import attention_segments
+    q, ks, vs = _case(1, 700, 3, [2000, 400], seed=8)
+    segs = [(k.to(DEV), v.to(DEV)) for k, v in zip(ks, vs)]
+    a = attention_segments(q.to(DEV), segs, num_splits=3)
+    b = attention_segments(q.to(DEV), segs, num_splits=3)
+    assert torch.equal(a, b)
+
+
+def test_errors_are_loud(lib):
+    from lbw_amd import attention_segments
+    q = torch.zeros(1, 4, 1, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        attention_segments(q, [(q, q)])
+
+
+def _full_size_subset(H, Lq, lk_cache, lk_chunk, heads, rows, seed):
+    from lbw_amd import attention_segments
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    q = torch.randn(1, Lq, H, 128, generator=g, device=DEV).to(torch.bfloat16)
+    kc = torch.randn(1, lk_cache, H, 128, generator=g, device=DEV).to(torch.bfloat16)
+    vc = torch.randn(1, lk_cache, H, 128, generator=g, device=DEV).to(torch.bfloat16)
+    kn = torch.randn(1, lk_chunk, H, 128, generator=g, device=DEV).to(torch.bfloat16)
+    vn = torch.randn(1, lk_chunk, H, 128, generator=g, device=DEV).to(torch.bfloat16)
+    out = attention_segments(q, [(kc, vc), (kn, vn)])
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out.float()).all())
+    sel = torch.randperm(Lq, generator=torch.Generator().manual_seed(seed))[:rows].sort().values
+    for h in heads:
+        qh = q[:, sel][:, :, h:h + 1].cpu()
+        k = torch.cat([kc[:, :, h:h + 1], kn[:, :, h:h + 1]], 1).cpu()
+        v = torch.cat([vc[:, :, h:h + 1], vn[:, :, h:h + 1]], 1).cpu()
+        ref = O.attention_ref(qh, k, v)
+        m = assert_parity(out[:, sel][:, :, h:h + 1], ref, f"head {h}")
+        print(f"head {h}: {m}")
+
+
+def test_full_size_wan13b_480p_chunk(lib):
+    """1.3B 480p: 3-frame chunk (4680 q) over 6 cached frames + chunk (14040 keys), 12 heads."""
+    _full_size_subset(12, 4680, 9360, 4680, heads=[0, 7, 11], rows=384, seed=1)
+
+
+def test_full_size_wan14b_720p_chunk(lib):
+    """14B 720p: 1-frame chunk (3600 q) over 12 cached frames + chunk (46800 keys), 40 heads."""
+    _full_size_subset(40, 3600, 43200, 3600, heads=[0, 19, 39], rows=256, seed=2)
