@@ -145,41 +145,48 @@ struct TileRegs<true> {
 // bf16 K: thread t loads rows (t>>4) + 16i, 16-byte column t&15.
 // fp8  K: thread t loads rows (t>>3) + 32i, 16-byte column t&7.
 // V (both): thread t loads keys 4(t>>4) + i, d octet t&15.
+// Branch-free: rows outside [vlo, vhi) load a valid row (clamped) and are zeroed after.
 template <bool FP8>
 __device__ __forceinline__ void load_tile(const TileInfo& ti, TileRegs<FP8>& tr) {
   const int t = threadIdx.x;
+  const int hi_row = ti.vhi - 1;
+  auto clampr = [&](int r) { return r < ti.vlo ? ti.vlo : (r > hi_row ? hi_row : r); };
   if constexpr (!FP8) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = (t >> 4) + 16 * i;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (row >= ti.vlo && row < ti.vhi)
-        val = *reinterpret_cast<const u32x4*>(ti.kbase + (ti.row0 + row) * ti.ks + (t & 15) * 16);
+      u32x4 val = *reinterpret_cast<const u32x4*>(ti.kbase + (ti.row0 + clampr(row)) * ti.ks + (t & 15) * 16);
+      const bool z = row < ti.vlo || row > hi_row;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) val[w] = z ? 0u : val[w];
       tr.k[i] = val;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 4 * (t >> 4) + i;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (row >= ti.vlo && row < ti.vhi)
-        val = *reinterpret_cast<const u32x4*>(ti.vbase + (ti.row0 + row) * ti.vs + (t & 15) * 16);
+      u32x4 val = *reinterpret_cast<const u32x4*>(ti.vbase + (ti.row0 + clampr(row)) * ti.vs + (t & 15) * 16);
+      const bool z = row < ti.vlo || row > hi_row;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) val[w] = z ? 0u : val[w];
       tr.v[i] = val;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int row = (t >> 3) + 32 * i;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (row >= ti.vlo && row < ti.vhi)
-        val = *reinterpret_cast<const u32x4*>(ti.kbase + (ti.row0 + row) * ti.ks + (t & 7) * 16);
+      u32x4 val = *reinterpret_cast<const u32x4*>(ti.kbase + (ti.row0 + clampr(row)) * ti.ks + (t & 7) * 16);
+      const bool z = row < ti.vlo || row > hi_row;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) val[w] = z ? 0u : val[w];
       tr.k[i] = val;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 4 * (t >> 4) + i;
-      u32x2 val = {0u, 0u};
-      if (row >= ti.vlo && row < ti.vhi)
-        val = *reinterpret_cast<const u32x2*>(ti.vbase + (ti.row0 + row) * ti.vs + (t & 15) * 8);
+      u32x2 val = *reinterpret_cast<const u32x2*>(ti.vbase + (ti.row0 + clampr(row)) * ti.vs + (t & 15) * 8);
+      const bool z = row < ti.vlo || row > hi_row;
+      val[0] = z ? 0u : val[0];
+      val[1] = z ? 0u : val[1];
       tr.v[i] = val;
     }
   }
@@ -256,6 +263,11 @@ __device__ __forceinline__ uint32_t e4m3_encode(float x) {
   return sign | (code > 0x7eu ? 0x7eu : code);
 }
 
+// e4m3fn code -> its value as fp32 (exact), via the same bit placement as e4m3_to_f32_scaled.
+__device__ __forceinline__ float e4m3_value(uint32_t c) {
+  return __uint_as_float(((c & 0x80u) << 24) | ((c & 0x7fu) << 20)) * TWO_POW_120;
+}
+
 // ------------------------------------------------------------------ the kernel
 template <bool FP8>
 __global__ void __launch_bounds__(NT, 1)
@@ -263,7 +275,7 @@ attn_fwd_kernel(const AttnKernelArgs a) {
   using C = Cfg<FP8>;
   extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hl = lane >> 5;  // k-group / row-half of this lane
   const int l32 = lane & 31;
 
@@ -288,11 +300,13 @@ attn_fwd_kernel(const AttnKernelArgs a) {
   const int t0 = split * per_split;
   const int t1 = min(n_tiles, t0 + per_split);
 
-  const int q0 = qt * BM + wave * 64;  // first query of this wave
+  const int q0 = qt * BM + wave * 64;  // first query of this wave (wave-uniform)
   const bool wave_active = q0 < a.Lq;
 
   // ---- Q fragments (B operand of S^T = K Q^T)
-  // bf16: [qb][d-slice s]: d = 16s + 8hl .. +7.  fp8: [qb][s]: d = 64s + 32hl .. +31 (codes).
+  // bf16: qf[qb][s], d = 16s + 8hl .. +7.
+  // fp8:  q = sq * (hi + lo/16) with hi, lo e4m3 codes; qf[qb][2s + j] holds hi codes of
+  //       d = 64s + 32hl + 16j .. +15, qf[qb][4 + 2s + j] the lo codes of the same d.
   u32x4 qf[2][8];
   float qscale[2] = {1.0f, 1.0f};
 #pragma unroll
@@ -309,7 +323,7 @@ attn_fwd_kernel(const AttnKernelArgs a) {
       }
     } else {
       const uint16_t* qp = a.q + a.qsb * b + a.qsl * (int64_t)q + a.qsh * h + 32 * hl;
-      u32x4 raw[8];  // [s*4 + c]: d = 64s + 32hl + 8c .. +7
+      u32x4 raw[8];  // raw[4s + c]: d = 64s + 32hl + 8c .. +7
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         u32x4 v = {0u, 0u, 0u, 0u};
@@ -327,19 +341,24 @@ attn_fwd_kernel(const AttnKernelArgs a) {
       const float inv = 1.0f / sq;
       qscale[qb] = sq;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        // 32 codes = 8 dwords for k-slice s; dwords 0..3 in qf[qb][2s], 4..7 in qf[qb][2s+1]
+      for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int dw = 0; dw < 8; ++dw) {
+        for (int dw = 0; dw < 8; ++dw) {  // dword dw of slice s: d offsets 4dw .. 4dw+3
           const u32x4& r = raw[4 * s + (dw >> 1)];
           const int w0 = (dw & 1) * 2;
-          const uint32_t c0 = e4m3_encode(bf16_lo(r[w0]) * inv);
-          const uint32_t c1 = e4m3_encode(bf16_hi(r[w0]) * inv);
-          const uint32_t c2 = e4m3_encode(bf16_lo(r[w0 + 1]) * inv);
-          const uint32_t c3 = e4m3_encode(bf16_hi(r[w0 + 1]) * inv);
-          qf[qb][2 * s + (dw >> 2)][dw & 3] = c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+          const float y[4] = {bf16_lo(r[w0]) * inv, bf16_hi(r[w0]) * inv,
+                              bf16_lo(r[w0 + 1]) * inv, bf16_hi(r[w0 + 1]) * inv};
+          uint32_t hw = 0, lw = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t hc = e4m3_encode(y[e]);
+            const uint32_t lc = e4m3_encode((y[e] - e4m3_value(hc)) * 16.0f);
+            hw |= hc << (8 * e);
+            lw |= lc << (8 * e);
+          }
+          qf[qb][2 * s + (dw >> 2)][dw & 3] = hw;
+          qf[qb][4 + 2 * s + (dw >> 2)][dw & 3] = lw;
         }
-      }
     }
   }
 
@@ -403,12 +422,19 @@ attn_fwd_kernel(const AttnKernelArgs a) {
                                 (int)k1[0], (int)k1[1], (int)k1[2], (int)k1[3]};
 #pragma unroll
               for (int qb = 0; qb < 2; ++qb) {
-                const u32x4& qa = qf[qb][2 * s];
-                const u32x4& qc = qf[qb][2 * s + 1];
-                const i32x8 qv = {(int)qa[0], (int)qa[1], (int)qa[2], (int)qa[3],
-                                  (int)qc[0], (int)qc[1], (int)qc[2], (int)qc[3]};
+                const u32x4& h0 = qf[qb][2 * s];
+                const u32x4& h1 = qf[qb][2 * s + 1];
+                const u32x4& l0 = qf[qb][4 + 2 * s];
+                const u32x4& l1 = qf[qb][4 + 2 * s + 1];
+                const i32x8 qh = {(int)h0[0], (int)h0[1], (int)h0[2], (int)h0[3],
+                                  (int)h1[0], (int)h1[1], (int)h1[2], (int)h1[3]};
+                const i32x8 ql = {(int)l0[0], (int)l0[1], (int)l0[2], (int)l0[3],
+                                  (int)l1[0], (int)l1[1], (int)l1[2], (int)l1[3]};
+                // e8m0 operand scales: 127 = 1, 123 = 2^-4 (the lo part was scaled by 16)
                 sacc[qb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                    kf, qv, sacc[qb], 0, 0, 0, 127, 0, 127);
+                    kf, qh, sacc[qb], 0, 0, 0, 127, 0, 127);
+                sacc[qb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                    kf, ql, sacc[qb], 0, 0, 0, 127, 0, 123);
               }
             }
           }
@@ -436,7 +462,41 @@ attn_fwd_kernel(const AttnKernelArgs a) {
             m_true[qb] = fmaxf(m_true[qb], mx);
             need |= (m_true[qb] > m_used[qb] + tau_raw);
           }
+          // P = exp2(S cc - m c) to bf16 (fp32 row sums), then O^T[db][qb] += V^T[db, kb] P^T[qb].
+          auto pv = [&]() {
+            u32x4 pf[2][2];  // [qb][m]
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+              // m_used is still -inf only while every key so far was masked: then p = 0.
+              const float mc = (m_used[qb] == -INFINITY) ? 0.0f : m_used[qb] * c;
+              float ls = lsum[qb];
+#pragma unroll
+              for (int m = 0; m < 2; ++m) {
+                u32x4 w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const float p0 = fast_exp2(__builtin_fmaf(sacc[qb][8 * m + 2 * e], cc[qb], -mc));
+                  const float p1 = fast_exp2(__builtin_fmaf(sacc[qb][8 * m + 2 * e + 1], cc[qb], -mc));
+                  w[e] = pack_bf16x2(p0, p1);
+                  ls += p0 + p1;
+                }
+                pf[qb][m] = w;
+              }
+              lsum[qb] = ls;
+            }
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int m = 0; m < 2; ++m) {
+                const u32x4 vf = *reinterpret_cast<const u32x4*>(
+                    vt + (32 * db + l32) * VT_ROW + (32 * kb + 16 * m + 8 * hl) * 2);
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb)
+                  oacc[qb][db] = mfma32x32x16(vf, pf[qb][m], oacc[qb][db]);
+              }
+          };
           if (__any(need)) {
+            // Rare: the row max outgrew the exponent reference. Rescale O and l first.
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
               const float alpha =
@@ -449,39 +509,7 @@ attn_fwd_kernel(const AttnKernelArgs a) {
                 for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= alpha;
             }
           }
-          u32x4 pf[2][2];  // [qb][m]
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            const float mc = (m_used[qb] == -INFINITY) ? 0.0f : m_used[qb] * c;
-            float ls = 0.0f;
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-              float p[8];
-#pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                p[e] = fast_exp2(__builtin_fmaf(sacc[qb][8 * m + e], cc[qb], -mc));
-                ls += p[e];
-              }
-              u32x4 w;
-              w[0] = pack_bf16x2(p[0], p[1]);
-              w[1] = pack_bf16x2(p[2], p[3]);
-              w[2] = pack_bf16x2(p[4], p[5]);
-              w[3] = pack_bf16x2(p[6], p[7]);
-              pf[qb][m] = w;
-            }
-            lsum[qb] += ls;
-          }
-          // ---- O^T[db][qb] += V^T[db, kb] P^T[qb]
-#pragma unroll
-          for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-              const u32x4 vf = *reinterpret_cast<const u32x4*>(
-                  vt + (32 * db + l32) * VT_ROW + (32 * kb + 16 * m + 8 * hl) * 2);
-#pragma unroll
-              for (int qb = 0; qb < 2; ++qb)
-                oacc[qb][db] = mfma32x32x16(vf, pf[qb][m], oacc[qb][db]);
-            }
+          pv();
         }
       }
 

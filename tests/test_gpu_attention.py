@@ -120,7 +120,7 @@ def test_cross_attention_masked_and_unmasked(lib):
     from lbw_amd import attention, cross_attention
     g = torch.Generator().manual_seed(7)
     B, Lq, H = 2, 333, 4
-    q = _rand((B, Lq, H, 128), g, 2.0)
+    q = _rand((B, Lq, H, 128), g)
     k = _rand((B, 512, H, 128), g)
     v = _rand((B, 512, H, 128), g)
     k_lens = torch.tensor([300, 512], dtype=torch.int32)
@@ -129,6 +129,13 @@ def test_cross_attention_masked_and_unmasked(lib):
     assert_parity(out, ref, "masked")
     out_u = attention(q.to(DEV), k.to(DEV), v.to(DEV), is_cross_attn=True)
     assert_parity(out_u, O.attention_ref(q, k, v), "unmasked")
+    # peaked rows (query gain 4): outputs approach single V rows, |o| up to ~4, where one bf16
+    # step is 2^-6; bound the error relative to the output's scale instead
+    q4 = (q.float() * 4).to(torch.bfloat16)
+    out4 = cross_attention(q4.to(DEV), k.to(DEV), v.to(DEV), k_lens=k_lens.to(DEV))
+    ref4 = O.attention_ref(q4, k, v, k_lens=k_lens)
+    d = (out4.float().cpu() - ref4).abs()
+    assert bool(torch.all(d <= 1e-2 * ref4.abs().clamp_min(1.0))), float(d.max())
 
 
 def test_deterministic_bitwise(lib):

@@ -2,9 +2,10 @@
 oracle's restatement of kernels/qk_post.py:88-141 and the grid of model_fast.py:878-931.
 
 Tolerance: the kernel follows the oracle's rounding sequence op for op except the order of
-the fp32 sum of squares, so an output may differ by one bf16 step where the normalised value
-sits on a rounding boundary: |diff| <= 2^-7 |ref| (+ tiny abs) everywhere and bit-identical
-on >= 99% of elements."""
+the fp32 sum of squares (and so possibly the last bit of the rsqrt), so where the normalised
+value sits on a bf16 rounding boundary one intermediate flips by one bf16 step; through the
+rotation and the final rounding that is at most two bf16 steps of the rotated pair's
+magnitude: |diff| <= 2^-5 * |pair| everywhere, and >= 99.9% of elements bit-identical."""
 import pytest
 import torch
 
@@ -18,9 +19,11 @@ def _check(out, ref, what):
     o = out.float().cpu()
     r = ref.float().cpu()
     d = (o - r).abs()
-    assert bool(torch.all(d <= r.abs() * 2.0 ** -7 + 1e-6)), (what, float(d.max()))
+    pair = r.view(*r.shape[:-1], -1, 2).norm(dim=-1, keepdim=True).expand(
+        *r.shape[:-1], r.shape[-1] // 2, 2).reshape(r.shape)
+    assert bool(torch.all(d <= pair * 2.0 ** -5 + 1e-6)), (what, float(d.max()))
     same = float((o == r).float().mean())
-    assert same >= 0.99, (what, same)
+    assert same >= 0.999, (what, same)
     return same
 
 
