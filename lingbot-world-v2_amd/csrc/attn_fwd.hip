@@ -35,18 +35,14 @@
 // dequantisation (q scale x k block scale) is folded into cc. V is dequantised (x its block
 // scale) to bf16 on its way into LDS and PV runs on the bf16 MFMA.
 
-#include "common.h"
-#include "attn_fwd.h"
+#include "attn_tiles.h"
 
 namespace lbw {
 
-constexpr int D = 128;
 constexpr int BM = 256;
-constexpr int BN = 64;
 constexpr int NT = 256;
 constexpr int VT_ROW = BN * 2 + 16;  // LDS bytes per V^T row (16 B pad: conflict-free reads)
 constexpr int VT_BYTES = D * VT_ROW;
-constexpr float TAU = 8.0f;           // lazy-rescale threshold, log2 units
 constexpr float TWO_POW_120 = 1.329227995784916e36f;
 
 template <bool FP8>
@@ -57,76 +53,6 @@ struct Cfg {
   static constexpr int BUF = K_BYTES + VT_BYTES;
   static constexpr int LDS = 2 * BUF;
 };
-
-// ------------------------------------------------------------------ tile walk over segments
-// Segment i contributes the local key range [la, lb) = ([lo, hi) n [start, start+len)) - start
-// and the tiles ft .. ceil(lb / BN) - 1 of its own 64-key grid.
-struct TileInfo {
-  const unsigned char* kbase;  // row 0 of the segment for (b, h)
-  const unsigned char* vbase;
-  int64_t ks, vs;              // row strides in bytes
-  int64_t row0;                // first segment-local row of the tile
-  int vlo, vhi;                // valid rows of the tile
-  float sk, sv;                // fp8 block scales
-};
-
-__device__ __forceinline__ int seg_tiles(const SegDesc& s, int64_t lo, int64_t hi, int64_t& la,
-                                         int64_t& lb) {
-  if (s.len <= 0) return 0;
-  const int64_t st = s.start, en = s.start + s.len;
-  const int64_t a = lo > st ? lo : st;
-  const int64_t e = hi < en ? hi : en;
-  if (e <= a) return 0;
-  la = a - st;
-  lb = e - st;
-  return (int)((lb + BN - 1) / BN - la / BN);
-}
-
-__device__ __forceinline__ int count_tiles(const AttnKernelArgs& a, int64_t lo, int64_t hi) {
-  int n = 0;
-#pragma unroll 1
-  for (int i = 0; i < a.nseg; ++i) {
-    int64_t la = 0, lb = 0;
-    n += seg_tiles(a.seg[i], lo, hi, la, lb);
-  }
-  return n;
-}
-
-template <bool FP8>
-__device__ __forceinline__ TileInfo tile_info(const AttnKernelArgs& a, int64_t lo, int64_t hi,
-                                              int g, int b, int h) {
-  // Find the segment holding tile g (uniform loop: descriptors are read on demand).
-  int cum = 0, i = 0;
-  int64_t la = 0, lb = 0;
-#pragma unroll 1
-  for (; i < a.nseg - 1; ++i) {
-    const int n = seg_tiles(a.seg[i], lo, hi, la, lb);
-    if (g < cum + n) break;
-    cum += n;
-  }
-  const SegDesc& s = a.seg[i];
-  seg_tiles(s, lo, hi, la, lb);
-  TileInfo ti;
-  const int64_t lt = la / BN + (g - cum);
-  constexpr int esz = Cfg<FP8>::ESZ;
-  ti.kbase = reinterpret_cast<const unsigned char*>(s.k) + (s.ksb * b + s.ksh * h) * esz;
-  ti.vbase = reinterpret_cast<const unsigned char*>(s.v) + (s.vsb * b + s.vsh * h) * esz;
-  ti.ks = s.ksl * esz;
-  ti.vs = s.vsl * esz;
-  ti.row0 = lt * BN;
-  const int64_t vlo = la - ti.row0, vhi = lb - ti.row0;
-  ti.vlo = vlo > 0 ? (int)vlo : 0;
-  ti.vhi = vhi < BN ? (int)vhi : BN;
-  if constexpr (FP8) {
-    const int64_t bi = ((int64_t)b * a.H + h) * s.nblk + lt;
-    ti.sk = s.ks[bi];
-    ti.sv = s.vs[bi];
-  } else {
-    ti.sk = 1.0f;
-    ti.sv = 1.0f;
-  }
-  return ti;
-}
 
 // ------------------------------------------------------------------ global -> LDS staging
 template <bool FP8>
@@ -145,50 +71,31 @@ struct TileRegs<true> {
 // bf16 K: thread t loads rows (t>>4) + 16i, 16-byte column t&15.
 // fp8  K: thread t loads rows (t>>3) + 32i, 16-byte column t&7.
 // V (both): thread t loads keys 4(t>>4) + i, d octet t&15.
-// Branch-free: rows outside [vlo, vhi) load a valid row (clamped) and are zeroed after.
+// Rows outside the tile's valid range [vlo, vhi) load a valid row instead (clamped): their
+// scores are masked to -inf and their probabilities are exactly 0, so the duplicate data
+// never contributes, and no load waits on a branch or a select of its result.
 template <bool FP8>
 __device__ __forceinline__ void load_tile(const TileInfo& ti, TileRegs<FP8>& tr) {
   const int t = threadIdx.x;
   const int hi_row = ti.vhi - 1;
-  auto clampr = [&](int r) { return r < ti.vlo ? ti.vlo : (r > hi_row ? hi_row : r); };
+  auto row_addr = [&](const unsigned char* base, int64_t stride, int r) {
+    r = r < ti.vlo ? ti.vlo : (r > hi_row ? hi_row : r);
+    return base + (ti.row0 + r) * stride;
+  };
   if constexpr (!FP8) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = (t >> 4) + 16 * i;
-      u32x4 val = *reinterpret_cast<const u32x4*>(ti.kbase + (ti.row0 + clampr(row)) * ti.ks + (t & 15) * 16);
-      const bool z = row < ti.vlo || row > hi_row;
+    for (int i = 0; i < 4; ++i)
+      tr.k[i] = *reinterpret_cast<const u32x4*>(row_addr(ti.kbase, ti.ks, (t >> 4) + 16 * i) + (t & 15) * 16);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) val[w] = z ? 0u : val[w];
-      tr.k[i] = val;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * (t >> 4) + i;
-      u32x4 val = *reinterpret_cast<const u32x4*>(ti.vbase + (ti.row0 + clampr(row)) * ti.vs + (t & 15) * 16);
-      const bool z = row < ti.vlo || row > hi_row;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) val[w] = z ? 0u : val[w];
-      tr.v[i] = val;
-    }
+    for (int i = 0; i < 4; ++i)
+      tr.v[i] = *reinterpret_cast<const u32x4*>(row_addr(ti.vbase, ti.vs, 4 * (t >> 4) + i) + (t & 15) * 16);
   } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int row = (t >> 3) + 32 * i;
-      u32x4 val = *reinterpret_cast<const u32x4*>(ti.kbase + (ti.row0 + clampr(row)) * ti.ks + (t & 7) * 16);
-      const bool z = row < ti.vlo || row > hi_row;
+    for (int i = 0; i < 2; ++i)
+      tr.k[i] = *reinterpret_cast<const u32x4*>(row_addr(ti.kbase, ti.ks, (t >> 3) + 32 * i) + (t & 7) * 16);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) val[w] = z ? 0u : val[w];
-      tr.k[i] = val;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * (t >> 4) + i;
-      u32x2 val = *reinterpret_cast<const u32x2*>(ti.vbase + (ti.row0 + clampr(row)) * ti.vs + (t & 15) * 8);
-      const bool z = row < ti.vlo || row > hi_row;
-      val[0] = z ? 0u : val[0];
-      val[1] = z ? 0u : val[1];
-      tr.v[i] = val;
-    }
+    for (int i = 0; i < 4; ++i)
+      tr.v[i] = *reinterpret_cast<const u32x2*>(row_addr(ti.vbase, ti.vs, 4 * (t >> 4) + i) + (t & 15) * 8);
   }
 }
 
@@ -377,7 +284,7 @@ attn_fwd_kernel(const AttnKernelArgs a) {
 
   if (t0 < t1) {
     TileRegs<FP8> tr;
-    TileInfo ti = tile_info<FP8>(a, lo, hi, t0, b, h);
+    TileInfo ti = tile_info<Cfg<FP8>::ESZ, FP8>(a, lo, hi, t0, b, h);
     load_tile<FP8>(ti, tr);
     store_tile<FP8>(lds, tr, ti.sv);
     __syncthreads();
@@ -389,7 +296,7 @@ attn_fwd_kernel(const AttnKernelArgs a) {
       const float sk = ti.sk;
       const bool has_next = (t + 1) < t1;
       if (has_next) {
-        ti = tile_info<FP8>(a, lo, hi, t + 1, b, h);
+        ti = tile_info<Cfg<FP8>::ESZ, FP8>(a, lo, hi, t + 1, b, h);
         load_tile<FP8>(ti, tr);
       }
 
@@ -621,9 +528,6 @@ static hipError_t launch_impl(const AttnKernelArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
-  return launch_impl<false>(a, stream);
-}
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {
   return launch_impl<true>(a, stream);
 }

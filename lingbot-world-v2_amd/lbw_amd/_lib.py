@@ -11,7 +11,8 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "liblbw_attn.so")
+# LBW_ATTN_LIB overrides the in-tree library (for comparing builds side by side).
+LIB_PATH = os.environ.get("LBW_ATTN_LIB") or os.path.join(_HERE, "liblbw_attn.so")
 
 MAX_KV_SEGMENTS = 8
 FP8_BLOCK = 64
