@@ -62,6 +62,58 @@ __device__ __forceinline__ void dma16(const unsigned char* src, unsigned char* l
 __device__ __forceinline__ void wait_vmcnt_le8() { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); }
 __device__ __forceinline__ void wait_vmcnt_0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Scores of keys outside the tile's valid rows [tvlo, tvhi) -> -inf (S^T register layout).
+__device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int tvhi, int hl) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int key = 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3);
+    if (key < tvlo || key >= tvhi) sc[r] = -INFINITY;
+  }
+}
+
+// Online-softmax step of one 32-query block over 32 keys, branch-free. Updates the running
+// max; when some row of the wave outgrew its exponent reference by more than TAU, every row
+// moves its reference to its running max (alpha = the factor O must be scaled by, returned
+// with `true`). P = exp2(s c - m c) is packed to bf16 in the PV B-operand order and the row
+// sum is rescaled and accumulated.
+__device__ __forceinline__ bool softmax_block(const floatx16& sc, float& m_true, float& m_used,
+                                              float& lsum, float c, float tau_raw, u32x4 (&pf)[2],
+                                              float& alpha) {
+  float mx = sc[0];
+#pragma unroll
+  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[r]);
+  mx = wave_max_xor32(mx);
+  m_true = fmaxf(m_true, mx);
+  const bool move = __any(m_true > m_used + tau_raw);
+  const float m_new = move ? m_true : m_used;
+  alpha = (!move || m_used == -INFINITY) ? (move ? 0.0f : 1.0f) : fast_exp2((m_used - m_new) * c);
+  m_used = m_new;
+  // m_used is still -inf only while every key so far was masked: then p = 0.
+  const float mc = (m_used == -INFINITY) ? 0.0f : m_used * c;
+  float ls = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float q0 = fast_exp2(__builtin_fmaf(sc[8 * m + 2 * e], c, -mc));
+      const float q1 = fast_exp2(__builtin_fmaf(sc[8 * m + 2 * e + 1], c, -mc));
+      w[e] = pack_bf16x2(q0, q1);
+      ls += q0 + q1;
+    }
+    pf[m] = w;
+  }
+  lsum = __builtin_fmaf(lsum, alpha, ls);
+  return move;
+}
+
+__device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+}
+
 __global__ void __launch_bounds__(NT, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
@@ -198,89 +250,64 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
       if (wave_active) {
         const int tvlo = vlo[0], tvhi = vhi[0];
-        const unsigned char* kt = cur;
-        const unsigned char* vt = cur + TILE_B;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-          // ---- S^T[qb] = K[kb] Q[qb]^T (32 keys x 32 queries per qb)
-          floatx16 sacc[2];
+          const unsigned char* kt = cur + kb * 32 * ROWB;
+          const unsigned char* vt = cur + TILE_B + kb * 32 * ROWB;
+          const bool partial = tvlo > 32 * kb || tvhi < 32 * kb + 32;
+          // phase 1: S0 = K Q0^T
+          u32x4 kf[8];
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
+          for (int s = 0; s < 8; ++s) kf[s] = *reinterpret_cast<const u32x4*>(kt + koff[s]);
+          floatx16 s0, s1;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[qb][r] = 0.0f;
+          for (int r = 0; r < 16; ++r) { s0[r] = 0.0f; s1[r] = 0.0f; }
 #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            const u32x4 kf = *reinterpret_cast<const u32x4*>(kt + kb * 32 * ROWB + koff[s]);
+          for (int s = 0; s < 8; ++s) s0 = mfma32x32x16(kf[s], qf[0][s], s0);
+          if (partial) mask_scores(s0, kb, tvlo, tvhi, hl);
+          // phase 2: S1 = K Q1^T  |  softmax of query block 0
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) sacc[qb] = mfma32x32x16(kf, qf[qb][s], sacc[qb]);
+          for (int s = 0; s < 8; ++s) s1 = mfma32x32x16(kf[s], qf[1][s], s1);
+          u32x4 p0[2];
+          float alpha0;
+          const bool r0 = softmax_block(s0, m_true[0], m_used[0], lsum[0], c, tau_raw, p0, alpha0);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // 8 VALU
           }
-          if (tvlo > 32 * kb || tvhi < 32 * kb + 32) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3);
-              if (key < tvlo || key >= tvhi) {
-                sacc[0][r] = -INFINITY;
-                sacc[1][r] = -INFINITY;
-              }
-            }
-          }
-          // ---- online softmax (lazy rescale)
-          bool need = false;
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[qb][r]);
-            mx = wave_max_xor32(mx);
-            m_true[qb] = fmaxf(m_true[qb], mx);
-            need |= (m_true[qb] > m_used[qb] + tau_raw);
-          }
-          if (__any(need)) {
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-              const float alpha =
-                  (m_used[qb] == -INFINITY) ? 0.0f : fast_exp2((m_used[qb] - m_true[qb]) * c);
-              m_used[qb] = m_true[qb];
-              lsum[qb] *= alpha;
-#pragma unroll
-              for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= alpha;
-            }
-          }
-          u32x4 pf[2][2];  // [qb][m]
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            // m_used is still -inf only while every key so far was masked: then p = 0.
-            const float mc = (m_used[qb] == -INFINITY) ? 0.0f : m_used[qb] * c;
-            float ls = lsum[qb];
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-              u32x4 w;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const float p0 = fast_exp2(__builtin_fmaf(sacc[qb][8 * m + 2 * e], c, -mc));
-                const float p1 = fast_exp2(__builtin_fmaf(sacc[qb][8 * m + 2 * e + 1], c, -mc));
-                w[e] = pack_bf16x2(p0, p1);
-                ls += p0 + p1;
-              }
-              pf[qb][m] = w;
-            }
-            lsum[qb] = ls;
-          }
-          // ---- O^T[db][qb] += V^T[db, kb] P^T[qb]
+          if (partial) mask_scores(s1, kb, tvlo, tvhi, hl);
+          if (r0) scale_acc(oacc[0], alpha0);
+          // phase 3: O0 += V^T P0^T  |  softmax of query block 1
+          u32x4 vf[4][2];
 #pragma unroll
           for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
-              const unsigned char* vb = vt + (32 * kb + 16 * m) * ROWB;
+              const unsigned char* vb = vt + 16 * m * ROWB;
               const u32x2 v0 = lds_read_tr16(vb + voff[db][0]);
               const u32x2 v1 = lds_read_tr16(vb + voff[db][1]);
-              const u32x4 vf = {v0[0], v0[1], v1[0], v1[1]};
-#pragma unroll
-              for (int qb = 0; qb < 2; ++qb)
-                oacc[qb][db] = mfma32x32x16(vf, pf[qb][m], oacc[qb][db]);
+              vf[db][m] = u32x4{v0[0], v0[1], v1[0], v1[1]};
             }
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) oacc[0][db] = mfma32x32x16(vf[db][m], p0[m], oacc[0][db]);
+          u32x4 p1[2];
+          float alpha1;
+          const bool r1 = softmax_block(s1, m_true[1], m_used[1], lsum[1], c, tau_raw, p1, alpha1);
+          __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);   // the V transpose reads first
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+          }
+          if (r1) scale_acc(oacc[1], alpha1);
+          // phase 4: O1 += V^T P1^T
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int m = 0; m < 2; ++m) oacc[1][db] = mfma32x32x16(vf[db][m], p1[m], oacc[1][db]);
         }
       }
 
