@@ -36,8 +36,7 @@
 namespace lbw {
 namespace {
 
-constexpr int BM = 256;
-constexpr int NT = 256;
+constexpr int BM = 256;                 // queries per workgroup
 constexpr int ROWB = D * 2;             // bytes per K/V row in LDS
 constexpr int TILE_B = BN * ROWB;       // 16 KB
 constexpr int STAGE_B = 2 * TILE_B;     // K tile + V tile
@@ -59,11 +58,19 @@ __device__ __forceinline__ void dma16(const unsigned char* src, unsigned char* l
   __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(lds_dst), 16, 0, 0);
 }
 
-__device__ __forceinline__ void wait_vmcnt_le8() { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_le() {
+  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else static_assert(N == 8 || N == 4, "vmcnt");
+}
 __device__ __forceinline__ void wait_vmcnt_0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Scores of keys outside the tile's valid rows [tvlo, tvhi) -> -inf (S^T register layout).
+// Called only for partial sub-blocks; the empty asm keeps the compiler from speculating the
+// masking into the full sub-blocks' path.
 __device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int tvhi, int hl) {
+  asm volatile("" ::: "memory");
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3);
@@ -114,8 +121,14 @@ __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
     for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
 }
 
-__global__ void __launch_bounds__(NT, 1)
+// NW waves per workgroup: 4 (64 queries = two 32-query blocks per wave, one wave per SIMD,
+// block-level interleaving in software) or 8 (32 queries per wave, two waves per SIMD that the
+// hardware interleaves).
+template <int NW>
+__global__ void __launch_bounds__(NW * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
+  constexpr int QB = 8 / NW;        // 32-query blocks per wave
+  constexpr int NDMA = 16 / NW;     // 1 KB DMA blocks per wave per K (and per V) tile
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -143,13 +156,13 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   const int t0 = split * per_split;
   const int t1 = min(n_tiles, t0 + per_split);
 
-  const int q0 = qt * BM + wave * 64;  // first query of this wave (wave-uniform)
+  const int q0 = qt * BM + wave * 32 * QB;  // first query of this wave (wave-uniform)
   const bool wave_active = q0 < a.Lq;
 
   // ---- Q fragments (B operand of S^T = K Q^T): qf[qb][s] holds d = 16s + 8hl .. +7
-  u32x4 qf[2][8];
+  u32x4 qf[QB][8];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const int q = q0 + 32 * qb + l32;
     const uint16_t* qp = a.q + a.qsb * b + a.qsl * (int64_t)q + a.qsh * h + 8 * hl;
 #pragma unroll
@@ -161,11 +174,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   }
 
   // ---- per-lane LDS offsets
-  // DMA: this wave fills 1 KB blocks 4*wave + i of each tile; lane -> (row, physical chunk).
-  int dma_row[4], dma_col[4];
+  // DMA: this wave fills 1 KB blocks NDMA*wave + i of each tile; lane -> (row, physical chunk).
+  int dma_row[NDMA], dma_col[NDMA];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    dma_row[i] = 16 * wave + 4 * i + (lane >> 4);
+  for (int i = 0; i < NDMA; ++i) {
+    dma_row[i] = 4 * (NDMA * wave + i) + (lane >> 4);
     dma_col[i] = ((lane & 15) ^ swz(dma_row[i])) * 16;  // byte offset of the logical chunk
   }
   // K fragment (kb = 0) for d-slice s: row l32, logical chunk 2s + hl.
@@ -187,16 +200,18 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
   }
 
-  floatx16 oacc[2][4];
+  floatx16 oacc[QB][4];
+  float m_used[QB], m_true[QB], lsum[QB];  // exponent reference, running row max, row sum
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) oacc[qb][db][r] = 0.0f;
-  float m_used[2] = {-INFINITY, -INFINITY};  // exponent reference
-  float m_true[2] = {-INFINITY, -INFINITY};  // running row max
-  float lsum[2] = {0.0f, 0.0f};
+    m_used[qb] = -INFINITY;
+    m_true[qb] = -INFINITY;
+    lsum[qb] = 0.0f;
+  }
   const float c = a.scale_log2;
   const float tau_raw = TAU / c;
 
@@ -208,11 +223,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     const unsigned char* vb = ti.vbase + ti.row0 * ti.vs;
     const int rlo = ti.vlo, rhi = ti.vhi - 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NDMA; ++i) {
       int r = dma_row[i];
       r = r < rlo ? rlo : (r > rhi ? rhi : r);
-      dma16(kb + r * ti.ks + dma_col[i], stage + 1024 * (4 * wave + i));
-      dma16(vb + r * ti.vs + dma_col[i], stage + TILE_B + 1024 * (4 * wave + i));
+      dma16(kb + r * ti.ks + dma_col[i], stage + 1024 * (NDMA * wave + i));
+      dma16(vb + r * ti.vs + dma_col[i], stage + TILE_B + 1024 * (NDMA * wave + i));
     }
   };
 
@@ -230,7 +245,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       vlo[1] = ti.vlo;
       vhi[1] = ti.vhi;
       issue(ti, lds + STAGE_B);
-      wait_vmcnt_le8();
+      wait_vmcnt_le<2 * NDMA>();
     } else {
       wait_vmcnt_0();
     }
@@ -250,69 +265,94 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
       if (wave_active) {
         const int tvlo = vlo[0], tvhi = vhi[0];
+        const unsigned char* vt0 = cur + TILE_B;
+        auto vfrag = [&](const unsigned char* vt, int db, int m) {
+          const unsigned char* vb = vt + 16 * m * ROWB;
+          const u32x2 v0 = lds_read_tr16(vb + voff[db][0]);
+          const u32x2 v1 = lds_read_tr16(vb + voff[db][1]);
+          return u32x4{v0[0], v0[1], v1[0], v1[1]};
+        };
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
           const unsigned char* kt = cur + kb * 32 * ROWB;
-          const unsigned char* vt = cur + TILE_B + kb * 32 * ROWB;
+          const unsigned char* vt = vt0 + kb * 32 * ROWB;
           const bool partial = tvlo > 32 * kb || tvhi < 32 * kb + 32;
-          // phase 1: S0 = K Q0^T
-          u32x4 kf[8];
+          if constexpr (QB == 2) {
+            // phase 1: S0 = K Q0^T
+            u32x4 kf[8];
 #pragma unroll
-          for (int s = 0; s < 8; ++s) kf[s] = *reinterpret_cast<const u32x4*>(kt + koff[s]);
-          floatx16 s0, s1;
+            for (int s = 0; s < 8; ++s) kf[s] = *reinterpret_cast<const u32x4*>(kt + koff[s]);
+            floatx16 s0, s1;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) { s0[r] = 0.0f; s1[r] = 0.0f; }
+            for (int r = 0; r < 16; ++r) { s0[r] = 0.0f; s1[r] = 0.0f; }
 #pragma unroll
-          for (int s = 0; s < 8; ++s) s0 = mfma32x32x16(kf[s], qf[0][s], s0);
-          if (partial) mask_scores(s0, kb, tvlo, tvhi, hl);
-          // phase 2: S1 = K Q1^T  |  softmax of query block 0
+            for (int s = 0; s < 8; ++s) s0 = mfma32x32x16(kf[s], qf[0][s], s0);
+            if (partial) mask_scores(s0, kb, tvlo, tvhi, hl);
+            // phase 2: S1 = K Q1^T  |  softmax of query block 0
 #pragma unroll
-          for (int s = 0; s < 8; ++s) s1 = mfma32x32x16(kf[s], qf[1][s], s1);
-          u32x4 p0[2];
-          float alpha0;
-          const bool r0 = softmax_block(s0, m_true[0], m_used[0], lsum[0], c, tau_raw, p0, alpha0);
+            for (int s = 0; s < 8; ++s) s1 = mfma32x32x16(kf[s], qf[QB - 1][s], s1);
+            u32x4 p0[2];
+            float alpha0;
+            const bool r0 = softmax_block(s0, m_true[0], m_used[0], lsum[0], c, tau_raw, p0, alpha0);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // 8 VALU
-          }
-          if (partial) mask_scores(s1, kb, tvlo, tvhi, hl);
-          if (r0) scale_acc(oacc[0], alpha0);
-          // phase 3: O0 += V^T P0^T  |  softmax of query block 1
-          u32x4 vf[4][2];
-#pragma unroll
-          for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int m = 0; m < 2; ++m) {
-              const unsigned char* vb = vt + 16 * m * ROWB;
-              const u32x2 v0 = lds_read_tr16(vb + voff[db][0]);
-              const u32x2 v1 = lds_read_tr16(vb + voff[db][1]);
-              vf[db][m] = u32x4{v0[0], v0[1], v1[0], v1[1]};
+            for (int i = 0; i < 8; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // 8 VALU
             }
+            if (partial) mask_scores(s1, kb, tvlo, tvhi, hl);
+            if (r0) scale_acc(oacc[0], alpha0);
+            // phase 3: O0 += V^T P0^T  |  softmax of query block 1
+            u32x4 vf[4][2];
 #pragma unroll
-          for (int db = 0; db < 4; ++db)
+            for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int m = 0; m < 2; ++m) oacc[0][db] = mfma32x32x16(vf[db][m], p0[m], oacc[0][db]);
-          u32x4 p1[2];
-          float alpha1;
-          const bool r1 = softmax_block(s1, m_true[1], m_used[1], lsum[1], c, tau_raw, p1, alpha1);
-          __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);   // the V transpose reads first
+              for (int m = 0; m < 2; ++m) vf[db][m] = vfrag(vt, db, m);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int m = 0; m < 2; ++m) oacc[0][db] = mfma32x32x16(vf[db][m], p0[m], oacc[0][db]);
+            u32x4 p1[2];
+            float alpha1;
+            const bool r1 = softmax_block(s1, m_true[QB - 1], m_used[QB - 1], lsum[QB - 1], c,
+                                          tau_raw, p1, alpha1);
+            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);   // the V transpose reads first
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            }
+            if (r1) scale_acc(oacc[QB - 1], alpha1);
+            // phase 4: O1 += V^T P1^T
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int m = 0; m < 2; ++m)
+                oacc[QB - 1][db] = mfma32x32x16(vf[db][m], p1[m], oacc[QB - 1][db]);
+          } else {
+            // one 32-query block: S = K Q^T, softmax, O += V^T P^T (the other wave on this
+            // SIMD fills the gaps)
+            floatx16 s0;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s0[r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 8; ++s)
+              s0 = mfma32x32x16(*reinterpret_cast<const u32x4*>(kt + koff[s]), qf[0][s], s0);
+            if (partial) mask_scores(s0, kb, tvlo, tvhi, hl);
+            u32x4 p0[2];
+            float alpha0;
+            const bool r0 = softmax_block(s0, m_true[0], m_used[0], lsum[0], c, tau_raw, p0, alpha0);
+            if (r0) scale_acc(oacc[0], alpha0);
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int m = 0; m < 2; ++m)
+                oacc[0][db] = mfma32x32x16(vfrag(vt, db, m), p0[m], oacc[0][db]);
           }
-          if (r1) scale_acc(oacc[1], alpha1);
-          // phase 4: O1 += V^T P1^T
-#pragma unroll
-          for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int m = 0; m < 2; ++m) oacc[1][db] = mfma32x32x16(vf[db][m], p1[m], oacc[1][db]);
         }
       }
 
       // tile t+1 must be in LDS for every wave before the next iteration
-      if (has2) wait_vmcnt_le8(); else wait_vmcnt_0();
+      if (has2) wait_vmcnt_le<2 * NDMA>(); else wait_vmcnt_0();
       __syncthreads();
       vlo[0] = vlo[1]; vhi[0] = vhi[1];
       vlo[1] = vlo[2]; vhi[1] = vhi[2];
@@ -324,7 +364,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
   // ---- epilogue
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < QB; ++qb) {
     const int q = q0 + 32 * qb + l32;
     const float l_tot = wave_sum_xor32(lsum[qb]);
     if (a.mode == kModeNormalized) {
@@ -376,13 +416,22 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel,
+template <int NW>
+static hipError_t launch_nw(const AttnKernelArgs& a, hipStream_t stream) {
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<NW>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t nwg = (uint32_t)a.n_qtiles * a.splits * a.H * a.B;
-  hipLaunchKernelGGL(attn_fwd_bf16_kernel, dim3(nwg), dim3(NT), LDS_B, stream, a);
+  hipLaunchKernelGGL(attn_fwd_bf16_kernel<NW>, dim3(nwg), dim3(NW * 64), LDS_B, stream, a);
   return hipGetLastError();
+}
+
+#ifndef LBW_ATTN_WAVES
+#define LBW_ATTN_WAVES 8
+#endif
+
+hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
+  return launch_nw<LBW_ATTN_WAVES>(a, stream);
 }
 
 }  // namespace lbw
