@@ -215,36 +215,51 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   const float c = a.scale_log2;
   const float tau_raw = TAU / c;
 
-  // Issue the DMA of one tile into a stage (8 x 16 B per lane). Rows outside the tile's
-  // valid range [vlo, vhi) fetch a valid row instead: their scores are masked to -inf and
-  // their probabilities are exactly 0, so the duplicate never contributes.
-  auto issue = [&](const TileInfo& ti, unsigned char* stage) {
-    const unsigned char* kb = ti.kbase + ti.row0 * ti.ks;
-    const unsigned char* vb = ti.vbase + ti.row0 * ti.vs;
-    const int rlo = ti.vlo, rhi = ti.vhi - 1;
+  // DMA of the cursor's tile into a stage (2*NDMA x 16 B per lane). Full tiles use the
+  // per-segment lane offsets; in a partial tile, rows outside the valid range [vlo, vhi)
+  // fetch a valid row instead: their scores are masked to -inf and their probabilities are
+  // exactly 0, so the duplicate never contributes.
+  TileCursor cs;
+  uint32_t lane_k[NDMA], lane_v[NDMA];
+  auto seg_offsets = [&]() {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
-      int r = dma_row[i];
-      r = r < rlo ? rlo : (r > rhi ? rhi : r);
-      dma16(kb + r * ti.ks + dma_col[i], stage + 1024 * (NDMA * wave + i));
-      dma16(vb + r * ti.vs + dma_col[i], stage + TILE_B + 1024 * (NDMA * wave + i));
+      lane_k[i] = (uint32_t)(dma_row[i] * cs.ks + dma_col[i]);
+      lane_v[i] = (uint32_t)(dma_row[i] * cs.vs + dma_col[i]);
     }
+  };
+  auto issue = [&](unsigned char* stage, int& tvlo, int& tvhi) {
+    cursor_rows(cs, tvlo, tvhi);
+    const int64_t row0 = cs.lt * BN;
+    const unsigned char* kb = cs.kbase + row0 * cs.ks;
+    const unsigned char* vb = cs.vbase + row0 * cs.vs;
+    if (tvlo == 0 && tvhi == BN) {
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) {
+        dma16(kb + lane_k[i], stage + 1024 * (NDMA * wave + i));
+        dma16(vb + lane_v[i], stage + TILE_B + 1024 * (NDMA * wave + i));
+      }
+    } else {
+      const int rhi = tvhi - 1;
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) {
+        int r = dma_row[i];
+        r = r < tvlo ? tvlo : (r > rhi ? rhi : r);
+        dma16(kb + r * cs.ks + dma_col[i], stage + 1024 * (NDMA * wave + i));
+        dma16(vb + r * cs.vs + dma_col[i], stage + TILE_B + 1024 * (NDMA * wave + i));
+      }
+    }
+    if (cursor_next<2>(a, lo, hi, b, h, cs) && cs.seg < a.nseg) seg_offsets();
   };
 
   if (t0 < t1) {
     // valid-row ranges of the tiles in flight: [0] = current, [1] = next, [2] = after next
     int vlo[3] = {0, 0, 0}, vhi[3] = {BN, BN, BN};
-    {
-      const TileInfo ti = tile_info<2, false>(a, lo, hi, t0, b, h);
-      vlo[0] = ti.vlo;
-      vhi[0] = ti.vhi;
-      issue(ti, lds);
-    }
+    cursor_init<2>(a, lo, hi, t0, b, h, cs);
+    seg_offsets();
+    issue(lds, vlo[0], vhi[0]);
     if (t0 + 1 < t1) {
-      const TileInfo ti = tile_info<2, false>(a, lo, hi, t0 + 1, b, h);
-      vlo[1] = ti.vlo;
-      vhi[1] = ti.vhi;
-      issue(ti, lds + STAGE_B);
+      issue(lds + STAGE_B, vlo[1], vhi[1]);
       wait_vmcnt_le<2 * NDMA>();
     } else {
       wait_vmcnt_0();
@@ -257,10 +272,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       const bool has2 = (t + 2) < t1;
       if (has2) {
         const int st2 = st >= 1 ? st - 1 : 2;  // (st + 2) % 3
-        const TileInfo ti = tile_info<2, false>(a, lo, hi, t + 2, b, h);
-        vlo[2] = ti.vlo;
-        vhi[2] = ti.vhi;
-        issue(ti, lds + st2 * STAGE_B);
+        issue(lds + st2 * STAGE_B, vlo[2], vhi[2]);
       }
 
       if (wave_active) {

@@ -81,4 +81,80 @@ __device__ __forceinline__ TileInfo tile_info(const AttnKernelArgs& a, int64_t l
   return ti;
 }
 
+// Sequential walk over the tiles of [lo, hi), in order. The segment descriptors (kernel
+// arguments) are read only when the walk enters a new segment, so stepping to the next tile
+// is a handful of scalar instructions.
+struct TileCursor {
+  int seg;                    // current segment; nseg when the walk is past the last tile
+  int64_t lt, lt_end;         // current and one-past-last local tile of the segment
+  int64_t la, lb;             // valid local key range of the segment
+  const unsigned char* kbase; // row 0 of the segment for (b, h)
+  const unsigned char* vbase;
+  int64_t ks, vs;             // row strides in bytes
+  const float* ksc;           // fp8 block scales of (b, h) (fp8 cache only)
+  const float* vsc;
+};
+
+template <int ESZ>
+__device__ __forceinline__ void cursor_enter(const AttnKernelArgs& a, int i, int64_t la,
+                                             int64_t lb, int b, int h, TileCursor& c) {
+  const SegDesc& s = a.seg[i];
+  c.seg = i;
+  c.la = la;
+  c.lb = lb;
+  c.lt = la / BN;
+  c.lt_end = (lb + BN - 1) / BN;
+  c.kbase = reinterpret_cast<const unsigned char*>(s.k) + (s.ksb * b + s.ksh * h) * ESZ;
+  c.vbase = reinterpret_cast<const unsigned char*>(s.v) + (s.vsb * b + s.vsh * h) * ESZ;
+  c.ks = s.ksl * ESZ;
+  c.vs = s.vsl * ESZ;
+  const int64_t so = ((int64_t)b * a.H + h) * s.nblk;
+  c.ksc = s.ks != nullptr ? s.ks + so : nullptr;
+  c.vsc = s.vs != nullptr ? s.vs + so : nullptr;
+}
+
+// Positions the cursor on tile g of the walk (the g-th tile holding keys of [lo, hi)).
+template <int ESZ>
+__device__ __forceinline__ void cursor_init(const AttnKernelArgs& a, int64_t lo, int64_t hi,
+                                            int g, int b, int h, TileCursor& c) {
+  int cum = 0;
+  c.seg = a.nseg;
+#pragma unroll 1
+  for (int i = 0; i < a.nseg; ++i) {
+    int64_t la = 0, lb = 0;
+    const int n = seg_tiles(a.seg[i], lo, hi, la, lb);
+    if (g < cum + n) {
+      cursor_enter<ESZ>(a, i, la, lb, b, h, c);
+      c.lt += g - cum;
+      return;
+    }
+    cum += n;
+  }
+}
+
+// Advances to the next tile; returns true when the cursor entered a new segment.
+template <int ESZ>
+__device__ __forceinline__ bool cursor_next(const AttnKernelArgs& a, int64_t lo, int64_t hi,
+                                            int b, int h, TileCursor& c) {
+  if (++c.lt < c.lt_end) return false;
+#pragma unroll 1
+  for (int i = c.seg + 1; i < a.nseg; ++i) {
+    int64_t la = 0, lb = 0;
+    if (seg_tiles(a.seg[i], lo, hi, la, lb) > 0) {
+      cursor_enter<ESZ>(a, i, la, lb, b, h, c);
+      return true;
+    }
+  }
+  c.seg = a.nseg;
+  return true;
+}
+
+// Valid rows [vlo, vhi) of the cursor's tile.
+__device__ __forceinline__ void cursor_rows(const TileCursor& c, int& vlo, int& vhi) {
+  const int64_t row0 = c.lt * BN;
+  const int64_t l = c.la - row0, u = c.lb - row0;
+  vlo = l > 0 ? (int)l : 0;
+  vhi = u < BN ? (int)u : BN;
+}
+
 }  // namespace lbw

@@ -103,6 +103,10 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
           (s.v_stride_b % el) || (s.v_stride_l % el) || (s.v_stride_h % el))
         return fail(LBW_ERR_INVALID, "segment %d: strides must be multiples of %lld elements", i,
                     (long long)el);
+      // a tile's 64 rows must be addressable with 32-bit offsets from its first row
+      const int64_t esz = fp8 ? 1 : 2;
+      if (s.k_stride_l * esz * 64 >= (int64_t(1) << 32) || s.v_stride_l * esz * 64 >= (int64_t(1) << 32))
+        return fail(LBW_ERR_UNSUPPORTED, "segment %d: row stride too large", i);
       if (fp8 && (s.k_scale == nullptr || s.v_scale == nullptr))
         return fail(LBW_ERR_INVALID, "segment %d: fp8 scales missing", i);
     }
