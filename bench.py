@@ -9,10 +9,18 @@ Synthetic N(0,1) inputs, random RMSNorm gammas. Metric: attention TFLOP/s (4 Lq 
 layer, softmax excluded) over the whole timed step, plus ms per chunk.
 
 Usage: python bench.py [--steps K] [--warmup W] [--layers N] [--no-cpu]
+
+HBM traffic of the attention call (roofline.traffic) comes from two rocprofv3 --pmc passes
+over ``bench.py --pmc-workload`` (FETCH_SIZE, then WRITE_SIZE), scaled by what the same counter
+reads for a plain 1 GiB copy in the same program, and summarised by
+``bench.py --pmc-summarize FETCH_DIR WRITE_DIR`` into profiles/; bench.py reports it when that
+summary is present.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import math
 import os
@@ -36,10 +44,24 @@ CACHED_FRAMES = 12
 LK = LQ * (CACHED_FRAMES + 1)               # 46800
 START_FRAME = CACHED_FRAMES
 EPS = 1e-6
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_fwd_bf16_wan14b_720p_traffic.txt")
+COPY_BYTES = 1 << 30
 
 
 def attn_flops() -> float:
     return 4.0 * LQ * LK * D * H
+
+
+def attn_bytes() -> float:
+    """Algorithmic HBM bytes of one attention call: Q and O [LQ, H, D] plus K and V [LK, H, D],
+    bf16, each touched once."""
+    return 2.0 * (2 * LQ + 2 * LK) * H * D
+
+
+def qk_bytes() -> float:
+    """Algorithmic HBM bytes of one fused q/k norm + RoPE call: q, k, v rows read, q', k', v
+    written (bf16), plus the two gamma vectors and the RoPE tables (negligible)."""
+    return 2.0 * 6 * LQ * C + 2 * 2 * C
 
 
 def build_layers(n_layers, dev):
@@ -102,6 +124,95 @@ def cpu_baseline(budget_s: float = 12.0):
                       f"ms per 40-layer chunk extrapolated: {dt / heads * H * 40 * 1e3:.0f}"}
 
 
+def pmc_workload():
+    """The program the --pmc passes profile: 3 layers' qk-norm/RoPE + attention calls of the
+    workload, then 3 plain copies of COPY_BYTES (calibration of the byte counters)."""
+    import torch
+    from lbw_amd import causal_rope_tables, wan_rope_freqs
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    layers = build_layers(1, dev)
+    tabs = causal_rope_tables(wan_rope_freqs(D), GRID, START_FRAME, device=dev)
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        run_layer(layers[0], tabs)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)     # the calibration copy: the last 3 dispatches
+    torch.cuda.synchronize()
+    print("pmc workload done", flush=True)
+
+
+def _pmc_rows(d, counter):
+    """Per-dispatch values of `counter` from a rocprofv3 --pmc csv output directory."""
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {d}")
+    rows = {}
+    for f in files:
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] != counter:
+                continue
+            k = int(r["Dispatch_Id"])
+            name, v = rows.get(k, (r["Kernel_Name"], 0.0))
+            rows[k] = (name, v + float(r["Counter_Value"]))
+    return [rows[k] for k in sorted(rows)]
+
+
+def pmc_summarize(fetch_dir, write_dir, cmds):
+    """Scale FETCH_SIZE / WRITE_SIZE (KiB per dispatch) by the calibration copy and write the
+    traffic summary that bench.py reports as roofline.traffic."""
+    out = {}
+    for key, d, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
+        rows = _pmc_rows(d, counter)
+        copy = [v for _, v in rows[-3:]]
+        factor = COPY_BYTES / (sum(copy) / len(copy) * 1024.0)
+        out[key + "_factor"] = factor
+        for tag, pat in (("attn_main", "attn_fwd_bf16"), ("attn_merge", "attn_merge"),
+                         ("qk_norm_rope", "qk_norm_rope")):
+            vals = [v for n, v in rows[:-3] if pat in n]
+            out[f"{tag}_{key}_bytes"] = (sum(vals) / len(vals) * 1024.0 * factor) if vals else 0.0
+            out[f"{tag}_dispatches"] = len(vals)
+    attn = sum(out[f"attn_{p}_{k}_bytes"] for p in ("main", "merge") for k in ("fetch", "write"))
+    qk = out["qk_norm_rope_fetch_bytes"] + out["qk_norm_rope_write_bytes"]
+    lines = [
+        "# HBM traffic per call, chunk attention at Wan-14B 720p (3600 q x 46800 k, 40 x 128, bf16)",
+        "# counters: rocprofv3 --pmc FETCH_SIZE, then --pmc WRITE_SIZE, KiB per dispatch, each",
+        "# scaled by (1 GiB / the counter's reading for a plain 1 GiB copy in the same program)",
+        "# commands (from /tmp, TMPDIR=/tmp):",
+        *[f"#   {c}" for c in cmds],
+        f"fetch_factor = {out['fetch_factor']:.4f}",
+        f"write_factor = {out['write_factor']:.4f}",
+    ]
+    for tag in ("attn_main", "attn_merge", "qk_norm_rope"):
+        lines.append(f"{tag}_fetch_bytes = {out[tag + '_fetch_bytes']:.0f}")
+        lines.append(f"{tag}_write_bytes = {out[tag + '_write_bytes']:.0f}")
+    lines += [f"attn_algorithmic_bytes = {attn_bytes():.0f}",
+              f"attn_traffic_bytes = {attn:.0f}",
+              f"attn_traffic_over_algorithmic = {attn / attn_bytes():.3f}",
+              f"qk_algorithmic_bytes = {qk_bytes():.0f}",
+              f"qk_traffic_bytes = {qk:.0f}",
+              f"qk_traffic_over_algorithmic = {qk / qk_bytes():.3f}"]
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def load_traffic():
+    """key = value figures of the committed traffic summary, or None."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    vals = {}
+    for line in open(TRAFFIC_FILE):
+        if "=" in line and not line.startswith("#"):
+            k, v = line.split("=", 1)
+            vals[k.strip()] = float(v)
+    return vals
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -110,11 +221,24 @@ def main():
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run the program profiled by the FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn the two --pmc outputs into the committed traffic summary")
+    ap.add_argument("--pmc-cmd", action="append", default=[],
+                    help="command lines recorded in the summary (with --pmc-summarize)")
     args = ap.parse_args()
+    if args.pmc_summarize:
+        pmc_summarize(*args.pmc_summarize, args.pmc_cmd)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU leg (run with --gpus 1)",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.pmc_workload:
+        pmc_workload()
+        return
 
     import torch
     from lbw_amd import causal_rope_tables, wan_rope_freqs
@@ -151,6 +275,7 @@ def main():
     flops_layer = attn_flops()
     value = flops_layer * len(layers) / (ms_step / 1e3) / 1e12
     achieved = flops_layer / (attn_ms / 1e3) / 1e12
+    tr = load_traffic()
 
     res = {
         "metric": "chunk self-attn TFLOP/s + ms/chunk (14B shape, 720p) and % of bf16 MFMA peak",
@@ -176,9 +301,15 @@ def main():
         "pct_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None,
-                     "kernel": "chunk attention call (attn_fwd_kernel + split merge)",
-                     "flops_per_launch": flops_layer},
+                     "traffic": round(tr["attn_traffic_bytes"]) if tr else None,
+                     "kernel": "chunk attention call (attn_fwd_bf16_kernel + split merge)",
+                     "flops_per_launch": flops_layer,
+                     "algorithmic_bytes_per_launch": attn_bytes()},
+        "qk_norm_rope_roofline": {"bound": "hbm",
+                                  "achieved": round(qk_bytes() / (qk_ms / 1e3) / 1e9, 1),
+                                  "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                  "frac": round(qk_bytes() / (qk_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+                                  "traffic": round(tr["qk_traffic_bytes"]) if tr else None},
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_budget)
