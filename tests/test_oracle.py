@@ -294,3 +294,65 @@ def test_fp8_quantizer_round_trip_and_scale_layout():
     z = torch.zeros(1, 64, 1, 8)
     c0, s0 = O.quantize_kv_fp8(z)
     assert torch.all(c0 == 0) and torch.all(s0 == 1)
+
+
+def test_layer_ref_zero_qk_weights_give_mean_of_values():
+    """Zero q/k projections and biases: q = k = RMSNorm(0) = 0, every score is 0, so each
+    output row is Wo (mean over all cached and chunk V rows) + bo."""
+    g = torch.Generator().manual_seed(21)
+    C, H = 256, 2
+    x = torch.randn(1, 12, C, generator=g)
+    xc = torch.randn(1, 24, C, generator=g)
+    z = torch.zeros(C, C)
+    zb = torch.zeros(C)
+    wv, wo = torch.randn(C, C, generator=g) * 0.05, torch.randn(C, C, generator=g) * 0.05
+    bv, bo = torch.randn(C, generator=g), torch.randn(C, generator=g)
+    out = O.self_attention_layer_ref(x, xc, z, zb, z, zb, wv, bv, wo, bo, torch.ones(C),
+                                     torch.ones(C), heads=H, grid=(1, 3, 4),
+                                     cache_grid=(2, 3, 4), start_frame=2)
+    vmean = (torch.cat([xc, x], 1)[0].double() @ wv.double().T + bv.double()).mean(0)
+    ref = vmean @ wo.double().T + bo.double()
+    assert torch.allclose(out[0].double(), ref.expand(12, C), atol=1e-5)
+
+
+def test_layer_ref_shifting_all_frames_changes_nothing():
+    """RoPE depends on position differences only: moving the chunk and the cached frames by
+    the same number of frames leaves the layer output unchanged (a wrong start_frame in either
+    the chunk's or the cache's grid breaks this)."""
+    g = torch.Generator().manual_seed(22)
+    C, H = 256, 2
+    x = torch.randn(1, 12, C, generator=g)
+    xc = torch.randn(1, 24, C, generator=g)
+    ws = [torch.randn(C, C, generator=g) * 0.1 for _ in range(4)]
+    bs = [torch.randn(C, generator=g) * 0.1 for _ in range(4)]
+    gq, gk = 1 + 0.1 * torch.randn(C, generator=g), 1 + 0.1 * torch.randn(C, generator=g)
+    args = (x, xc, ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], ws[3], bs[3], gq, gk)
+    a = O.self_attention_layer_ref(*args, heads=H, grid=(1, 3, 4), cache_grid=(2, 3, 4),
+                                   start_frame=2, cache_start_frame=0)
+    b = O.self_attention_layer_ref(*args, heads=H, grid=(1, 3, 4), cache_grid=(2, 3, 4),
+                                   start_frame=9, cache_start_frame=7)
+    c = O.self_attention_layer_ref(*args, heads=H, grid=(1, 3, 4), cache_grid=(2, 3, 4),
+                                   start_frame=3, cache_start_frame=0)
+    assert torch.allclose(a, b, atol=2e-5)
+    assert not torch.allclose(a, c, atol=1e-3)
+
+
+def test_cross_kv_ref_closed_forms():
+    """K = RMSNorm(ctx Wk + bk) is scale invariant (bk = 0) and zero for a zero context;
+    V = ctx Wv + bv is affine."""
+    g = torch.Generator().manual_seed(23)
+    C, H = 256, 2
+    ctx = torch.randn(1, 10, C, generator=g)
+    ctx[:, 7:] = 0
+    wk, wv = torch.randn(C, C, generator=g) * 0.05, torch.randn(C, C, generator=g) * 0.05
+    bv = torch.randn(C, generator=g)
+    gk = 1 + 0.1 * torch.randn(C, generator=g)
+    k1, v1 = O.cross_kv_ref(ctx, wk, torch.zeros(C), wv, bv, gk, H)
+    k3, v3 = O.cross_kv_ref(3 * ctx, wk, torch.zeros(C), wv, bv, gk, H)
+    assert torch.allclose(k1[:, :7], k3[:, :7], atol=1e-5)
+    assert torch.all(k1[:, 7:] == 0)
+    assert torch.allclose(v1[:, 7:], bv.view(1, 1, H, -1).expand(1, 3, H, C // H))
+    assert torch.allclose((v3 - bv.view(H, -1)), 3 * (v1 - bv.view(H, -1)), atol=1e-4)
+    # per-row RMS of K / gamma is 1 (the norm's defining property)
+    kk = (k1[0, :7].reshape(7, C) / gk)
+    assert torch.allclose(kk.pow(2).mean(-1), torch.ones(7), atol=1e-4)
