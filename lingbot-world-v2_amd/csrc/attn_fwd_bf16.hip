@@ -264,7 +264,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     } else {
       wait_vmcnt_0();
     }
-    __syncthreads();
+    barrier_nofence();
 
     int st = 0;  // stage of tile t
     for (int t = t0; t < t1; ++t) {
@@ -365,7 +365,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
       // tile t+1 must be in LDS for every wave before the next iteration
       if (has2) wait_vmcnt_le<2 * NDMA>(); else wait_vmcnt_0();
-      __syncthreads();
+      barrier_nofence();
       vlo[0] = vlo[1]; vhi[0] = vhi[1];
       vlo[1] = vlo[2]; vhi[1] = vhi[2];
       st = st == 2 ? 0 : st + 1;

@@ -41,10 +41,28 @@ __device__ __forceinline__ floatx16 mfma32x32x16(const u32x4& a, const u32x4& b,
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// Lane l and lane l^32 exchange through v_permlane32_swap (VALU, no LDS round trip): the swap
+// of (v, v) leaves the low half's value in one result and the high half's in the other, in
+// every lane.
 __device__ __forceinline__ float wave_max_xor32(float v) {
-  return fmaxf(v, __shfl_xor(v, 32));
+  const u32x2 r = __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false));
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float wave_sum_xor32(float v) { return v + __shfl_xor(v, 32); }
+__device__ __forceinline__ float wave_sum_xor32(float v) {
+  const u32x2 r = __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false));
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroup barrier without __syncthreads()'s memory fence, so outstanding global loads (the
+// K/V prefetch) stay in flight across it. Callers wait for the loads they need themselves; the
+// empty asm statements keep the compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void barrier_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ float wave_reduce_sum(float v) {
 #pragma unroll
