@@ -6,14 +6,16 @@
 // attention.py:1048-1058: out = softmax(scale * Q K^T) V over keys [lo, hi) of the
 // concatenated segments; a query row with no keys yields 0 (as torch's SDPA does).
 //
-// Work decomposition: one workgroup = 4 waves = 256 queries of one (batch, head) and one KV
-// split; each wave owns 64 queries (two 32-query MFMA blocks). K and V stream through LDS in
-// 64-key tiles with three stages in flight.
+// Work decomposition: one workgroup = 8 waves = 256 queries of one (batch, head) and one KV
+// split; each wave owns 32 queries, two waves share a SIMD. K and V stream through LDS in
+// 64-key tiles, NSTAGE tiles resident or in flight.
 //
 // Staging: tiles are copied HBM -> LDS by the direct global-to-LDS load (16 bytes per lane,
 // no registers, no VALU), K and V both kept row-major ([key][d], 256 B per row). Each 16-byte
 // chunk c of row r is stored at chunk c ^ swz(r), swz(r) = 4(r & 3) + ((r >> 2) & 3), which
-// makes both LDS read patterns below conflict-free.
+// makes both LDS read patterns below conflict-free. The K tiles of all stages sit in the
+// first 64 KB and the V tiles from 64 KB on, so with the stage known at compile time every
+// LDS read is a per-lane base register plus an immediate offset.
 //
 // Transposed formulation: S^T = K Q^T (A = K rows, ds_read_b128; B = Q from registers) and
 // O^T = V^T P^T (A = V^T via the LDS transpose read ds_read_b64_tr_b16; B = P^T straight
@@ -26,9 +28,13 @@
 // K..K+3 of column d0 + i when source lane s points at row K + s/4, columns d0 + 4(s%4)..+3;
 // two such reads (K = 16m + 4h and 16m + 4h + 8) fill the 8 k-values in exactly that order.
 //
+// Software pipeline (per wave, 32-key sub-blocks j): step j computes the softmax of S_j
+// (VALU) while the MFMA pipe runs O += V_{j-1}^T P_{j-1}^T and S_{j+1} = K_{j+1} Q^T, so the
+// VALU and MFMA work of one wave overlap; the second wave on the SIMD fills what is left.
+//
 // Online softmax in base 2 with the scale folded into one FMA: p = exp2(s*c - m*c),
 // c = scale*log2(e). The exponent reference m is only raised when the running max exceeds it
-// by more than 8 (log2 units), so P <= 256 and the O rescale is skipped on almost every tile;
+// by more than 8 (log2 units), so P <= 256 and the O rescale is skipped on almost every step;
 // O and l share the reference, so the final O / l is exact.
 
 #include "attn_tiles.h"
@@ -36,39 +42,84 @@
 namespace lbw {
 namespace {
 
-constexpr int BM = 256;                 // queries per workgroup
+#ifndef LBW_ATTN_NSTAGE
+#define LBW_ATTN_NSTAGE 3
+#endif
+#ifndef LBW_ATTN_LDS_AHEAD
+#define LBW_ATTN_LDS_AHEAD 2
+#endif
+#ifndef LBW_ATTN_VALU_A
+#define LBW_ATTN_VALU_A 4
+#endif
+#ifndef LBW_ATTN_VALU_B
+#define LBW_ATTN_VALU_B 4
+#endif
+#ifndef LBW_ATTN_XSTEP
+#define LBW_ATTN_XSTEP 0
+#endif
+#ifndef LBW_ATTN_DOT2_SUM
+#define LBW_ATTN_DOT2_SUM 0
+#endif
+
+constexpr int NWAVE = 8;                // waves per workgroup (32 queries each)
+constexpr int BM = 32 * NWAVE;          // queries per workgroup
 constexpr int ROWB = D * 2;             // bytes per K/V row in LDS
 constexpr int TILE_B = BN * ROWB;       // 16 KB
-constexpr int STAGE_B = 2 * TILE_B;     // K tile + V tile
-constexpr int NSTAGE = 3;
-constexpr int LDS_B = NSTAGE * STAGE_B; // 96 KB
+constexpr int HALF_B = TILE_B / 2;      // one 32-key sub-block
+constexpr int NSTAGE = LBW_ATTN_NSTAGE; // tiles resident or in flight
+constexpr int V_BASE = 65536;           // V tiles start here; K tiles at NSTAGE * 16 KB below
+constexpr int LDS_B = V_BASE + NSTAGE * TILE_B;
+constexpr int NDMA = TILE_B / (NWAVE * 64 * 16);  // 16-byte DMA blocks per lane per K/V tile
+constexpr int LDS_AHEAD = LBW_ATTN_LDS_AHEAD;     // MFMA pairs of LDS fragments in flight
+static_assert(NSTAGE >= 3 && NSTAGE <= 4, "LDS stages");
+static_assert(NSTAGE * TILE_B <= V_BASE, "K tiles must fit below the V tiles");
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
-typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ __forceinline__ u32x2 lds_read_tr16(const unsigned char* p) {
-  const shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(p));
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+
+// LDS reads at an integer LDS byte address, so the constant part of an address folds into the
+// instruction's offset field.
+__device__ __forceinline__ u32x2 lds_read_tr16(int addr) {
+  const shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(uintptr_t)addr);
   return __builtin_bit_cast(u32x2, v);
 }
-
-__device__ __forceinline__ void dma16(const unsigned char* src, unsigned char* lds_dst) {
-  __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(lds_dst), 16, 0, 0);
+__device__ __forceinline__ u32x4 lds_read_b128(int addr) {
+  return *(const lds_u32x4*)(uintptr_t)addr;
 }
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_le() {
-  if constexpr (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  else static_assert(N == 8 || N == 4, "vmcnt");
+// 16 bytes per lane HBM -> LDS (global_load_lds_dwordx4): lane l's bytes from sbase + voff land
+// at LDS byte address lds_dst + 16 l. Inline asm rather than the builtin: the compiler's wait
+// insertion treats an in-flight builtin copy as a hazard for every later LDS transpose read and
+// waits for all copies before each one, which would serialise the prefetch. The kernel waits
+// for the tiles it reads itself (wait_tiles_outstanding, then a barrier).
+__device__ __forceinline__ void dma16(const unsigned char* sbase, uint32_t voff, uint32_t lds_dst) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_dst) : "memory");
 }
-__device__ __forceinline__ void wait_vmcnt_0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)p;
+}
+
+// Waits until at most `n` tiles' DMA groups (2*NDMA loads each) of this wave are in flight.
+__device__ __forceinline__ void wait_tiles_outstanding(int n) {
+  static_assert(2 * NDMA == 4, "vmcnt immediates below assume 4 loads per tile");
+  if (n <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if (n == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+}
+
+// Hides a value from the optimiser (keeps a base register from being re-associated with
+// constant offsets that would no longer fit the 16-bit LDS immediate).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 // Scores of keys outside the tile's valid rows [tvlo, tvhi) -> -inf (S^T register layout).
-// Called only for partial sub-blocks; the empty asm keeps the compiler from speculating the
-// masking into the full sub-blocks' path.
 __device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int tvhi, int hl) {
   asm volatile("" ::: "memory");
 #pragma unroll
@@ -78,40 +129,10 @@ __device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int 
   }
 }
 
-// Online-softmax step of one 32-query block over 32 keys, branch-free. Updates the running
-// max; when some row of the wave outgrew its exponent reference by more than TAU, every row
-// moves its reference to its running max (alpha = the factor O must be scaled by, returned
-// with `true`). P = exp2(s c - m c) is packed to bf16 in the PV B-operand order and the row
-// sum is rescaled and accumulated.
-__device__ __forceinline__ bool softmax_block(const floatx16& sc, float& m_true, float& m_used,
-                                              float& lsum, float c, float tau_raw, u32x4 (&pf)[2],
-                                              float& alpha) {
-  float mx = sc[0];
-#pragma unroll
-  for (int r = 1; r < 16; ++r) mx = fmaxf(mx, sc[r]);
-  mx = wave_max_xor32(mx);
-  m_true = fmaxf(m_true, mx);
-  const bool move = __any(m_true > m_used + tau_raw);
-  const float m_new = move ? m_true : m_used;
-  alpha = (!move || m_used == -INFINITY) ? (move ? 0.0f : 1.0f) : fast_exp2((m_used - m_new) * c);
-  m_used = m_new;
-  // m_used is still -inf only while every key so far was masked: then p = 0.
-  const float mc = (m_used == -INFINITY) ? 0.0f : m_used * c;
-  float ls = 0.0f;
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    u32x4 w;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float q0 = fast_exp2(__builtin_fmaf(sc[8 * m + 2 * e], c, -mc));
-      const float q1 = fast_exp2(__builtin_fmaf(sc[8 * m + 2 * e + 1], c, -mc));
-      w[e] = pack_bf16x2(q0, q1);
-      ls += q0 + q1;
-    }
-    pf[m] = w;
-  }
-  lsum = __builtin_fmaf(lsum, alpha, ls);
-  return move;
+// acc + lo(p) + hi(p) for a packed bf16 pair (v_dot2c_f32_bf16 against (1.0, 1.0)).
+__device__ __forceinline__ float dot2_bf16_ones(uint32_t p, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p),
+                                         __builtin_bit_cast(bf16x2, 0x3F803F80u), acc, false);
 }
 
 __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
@@ -121,14 +142,8 @@ __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
     for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
 }
 
-// NW waves per workgroup: 4 (64 queries = two 32-query blocks per wave, one wave per SIMD,
-// block-level interleaving in software) or 8 (32 queries per wave, two waves per SIMD that the
-// hardware interleaves).
-template <int NW>
-__global__ void __launch_bounds__(NW * 64, 1)
+__global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
-  constexpr int QB = 8 / NW;        // 32-query blocks per wave
-  constexpr int NDMA = 16 / NW;     // 1 KB DMA blocks per wave per K (and per V) tile
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -156,21 +171,23 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   const int t0 = split * per_split;
   const int t1 = min(n_tiles, t0 + per_split);
 
-  const int q0 = qt * BM + wave * 32 * QB;  // first query of this wave (wave-uniform)
+  const int q0 = qt * BM + wave * 32;  // first query of this wave (wave-uniform)
   const bool wave_active = q0 < a.Lq;
 
-  // ---- Q fragments (B operand of S^T = K Q^T): qf[qb][s] holds d = 16s + 8hl .. +7
-  u32x4 qf[QB][8];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int q = q0 + 32 * qb + l32;
+  // ---- Q fragments (B operand of S^T = K Q^T): qf[s] holds d = 16s + 8hl .. +7
+  u32x4 qf[8];
+  {
+    const int q = q0 + l32;
     const uint16_t* qp = a.q + a.qsb * b + a.qsl * (int64_t)q + a.qsh * h + 8 * hl;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (q < a.Lq) v = *reinterpret_cast<const u32x4*>(qp + 16 * s);
-      qf[qb][s] = v;
+      qf[s] = v;
     }
+    // Wait for Q here, on every path: otherwise the compiler, which cannot see the asm K/V
+    // copies, re-waits for all memory before the first MFMA of every loop iteration.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   }
 
   // ---- per-lane LDS offsets
@@ -181,12 +198,15 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     dma_row[i] = 4 * (NDMA * wave + i) + (lane >> 4);
     dma_col[i] = ((lane & 15) ^ swz(dma_row[i])) * 16;  // byte offset of the logical chunk
   }
-  // K fragment (kb = 0) for d-slice s: row l32, logical chunk 2s + hl.
+  // LDS byte addresses of this lane's fragments in stage 0.
+  // K fragment (sub-block rows 0..31) for d-slice s: row l32, logical chunk 2s + hl.
+  const int lds0 = (int)lds_addr(lds);
   int koff[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) koff[s] = l32 * ROWB + (((2 * s + hl) ^ swz(l32)) << 4);
-  // V transpose reads (kb = m = 0) for d-block db and key half j: source row
-  // 4hl + 8j + s/4, columns 32db + 16g + 4(s%4) .. +3 (s = lane % 16, g = (lane / 16) % 2).
+  for (int s = 0; s < 8; ++s) koff[s] = opaque(lds0 + l32 * ROWB + (((2 * s + hl) ^ swz(l32)) << 4));
+  // V transpose reads (sub-block rows 0..31, k-step m = 0) for d-block db and key
+  // half j: source row 4hl + 8j + s/4, columns 32db + 16g + 4(s%4) .. +3 (s = lane % 16,
+  // g = (lane / 16) % 2).
   int voff[4][2];
   {
     const int s16 = lane & 15, g = (lane >> 4) & 1;
@@ -196,29 +216,23 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       for (int j = 0; j < 2; ++j) {
         const int r = 4 * hl + 8 * j + (s16 >> 2);
         const int lc = 4 * db + 2 * g + ((s16 & 3) >> 1);
-        voff[db][j] = r * ROWB + ((lc ^ swz(r)) << 4) + 8 * (s16 & 1);
+        voff[db][j] = opaque(lds0 + V_BASE + r * ROWB + ((lc ^ swz(r)) << 4) + 8 * (s16 & 1));
       }
   }
 
-  floatx16 oacc[QB][4];
-  float m_used[QB], m_true[QB], lsum[QB];  // exponent reference, running row max, row sum
+  floatx16 oacc[4];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
+  for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[qb][db][r] = 0.0f;
-    m_used[qb] = -INFINITY;
-    m_true[qb] = -INFINITY;
-    lsum[qb] = 0.0f;
-  }
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
+  float m_used = -INFINITY, m_true = -INFINITY, lsum = 0.0f;  // exponent ref, row max, row sum
   const float c = a.scale_log2;
   const float tau_raw = TAU / c;
 
-  // DMA of the cursor's tile into a stage (2*NDMA x 16 B per lane). Full tiles use the
-  // per-segment lane offsets; in a partial tile, rows outside the valid range [vlo, vhi)
-  // fetch a valid row instead: their scores are masked to -inf and their probabilities are
-  // exactly 0, so the duplicate never contributes.
+  // DMA of the cursor's tile into a stage (2*NDMA x 16 B per lane); returns the tile's valid
+  // rows packed as vlo | vhi << 16. Full tiles use the per-segment lane offsets; in a partial
+  // tile, rows outside the valid range fetch a valid row instead: their scores are masked to
+  // -inf and their probabilities are exactly 0, so the duplicate never contributes.
   TileCursor cs;
   uint32_t lane_k[NDMA], lane_v[NDMA];
   auto seg_offsets = [&]() {
@@ -228,16 +242,20 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       lane_v[i] = (uint32_t)(dma_row[i] * cs.vs + dma_col[i]);
     }
   };
-  auto issue = [&](unsigned char* stage, int& tvlo, int& tvhi) {
+  const uint32_t lds_wave = lds_addr(lds) + 1024 * NDMA * wave;  // this wave's 1 KB blocks
+  auto issue = [&](int stage) -> int {
+    int tvlo, tvhi;
     cursor_rows(cs, tvlo, tvhi);
     const int64_t row0 = cs.lt * BN;
     const unsigned char* kb = cs.kbase + row0 * cs.ks;
     const unsigned char* vb = cs.vbase + row0 * cs.vs;
+    const uint32_t kdst = lds_wave + stage * TILE_B;
+    const uint32_t vdst = kdst + V_BASE;
     if (tvlo == 0 && tvhi == BN) {
 #pragma unroll
       for (int i = 0; i < NDMA; ++i) {
-        dma16(kb + lane_k[i], stage + 1024 * (NDMA * wave + i));
-        dma16(vb + lane_v[i], stage + TILE_B + 1024 * (NDMA * wave + i));
+        dma16(kb, lane_k[i], kdst + 1024 * i);
+        dma16(vb, lane_v[i], vdst + 1024 * i);
       }
     } else {
       const int rhi = tvhi - 1;
@@ -245,182 +263,258 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       for (int i = 0; i < NDMA; ++i) {
         int r = dma_row[i];
         r = r < tvlo ? tvlo : (r > rhi ? rhi : r);
-        dma16(kb + r * cs.ks + dma_col[i], stage + 1024 * (NDMA * wave + i));
-        dma16(vb + r * cs.vs + dma_col[i], stage + TILE_B + 1024 * (NDMA * wave + i));
+        dma16(kb, (uint32_t)(r * cs.ks) + dma_col[i], kdst + 1024 * i);
+        dma16(vb, (uint32_t)(r * cs.vs) + dma_col[i], vdst + 1024 * i);
       }
     }
     if (cursor_next<2>(a, lo, hi, b, h, cs) && cs.seg < a.nseg) seg_offsets();
+    return tvlo | (tvhi << 16);
   };
 
-  if (t0 < t1) {
-    // valid-row ranges of the tiles in flight: [0] = current, [1] = next, [2] = after next
-    int vlo[3] = {0, 0, 0}, vhi[3] = {BN, BN, BN};
+  const int T = t1 - t0;
+  if (T > 0) {
+    int vr[NSTAGE];  // valid rows of tiles u .. u+NSTAGE-1 (u = the tile being softmaxed)
+#pragma unroll
+    for (int k = 0; k < NSTAGE; ++k) vr[k] = BN << 16;
     cursor_init<2>(a, lo, hi, t0, b, h, cs);
     seg_offsets();
-    issue(lds, vlo[0], vhi[0]);
-    if (t0 + 1 < t1) {
-      issue(lds + STAGE_B, vlo[1], vhi[1]);
-      wait_vmcnt_le<2 * NDMA>();
-    } else {
-      wait_vmcnt_0();
+#pragma unroll
+    for (int k = 0; k < NSTAGE - 1; ++k)
+      if (k < T) vr[k] = issue(k);
+    // The first step's "previous sub-block" is the second half of stage NSTAGE-1's V tile
+    // with P = 0: zero it so that 0 * V stays 0 (that stage is only filled after barrier 0).
+    {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      unsigned char* zv = lds + V_BASE + (NSTAGE - 1) * TILE_B + HALF_B;
+      *reinterpret_cast<u32x4*>(zv + 16 * threadIdx.x) = z;
     }
+    wait_tiles_outstanding(min(NSTAGE - 2, T - 1));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero fill is done
     barrier_nofence();
 
-    int st = 0;  // stage of tile t
-    for (int t = t0; t < t1; ++t) {
-      unsigned char* cur = lds + st * STAGE_B;
-      const bool has2 = (t + 2) < t1;
-      if (has2) {
-        const int st2 = st >= 1 ? st - 1 : 2;  // (st + 2) % 3
-        issue(lds + st2 * STAGE_B, vlo[2], vhi[2]);
-      }
+    // Pipeline registers, double-buffered so that consecutive steps swap roles instead of
+    // copying: S of the sub-block being softmaxed / being computed, P of the previous / current
+    // sub-block. `pend` / `alpha_p`: an O rescale decided by the previous step, applied at the
+    // start of the next one (after the PV MFMAs that still used the old reference).
+    floatx16 sA, sB;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) { sA[r] = 0.0f; sB[r] = 0.0f; }
+    u32x4 pA[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    u32x4 pB[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    bool pend = false;
+    float alpha_p = 1.0f;
 
-      if (wave_active) {
-        const int tvlo = vlo[0], tvhi = vhi[0];
-        const unsigned char* vt0 = cur + TILE_B;
-        auto vfrag = [&](const unsigned char* vt, int db, int m) {
-          const unsigned char* vb = vt + 16 * m * ROWB;
-          const u32x2 v0 = lds_read_tr16(vb + voff[db][0]);
-          const u32x2 v1 = lds_read_tr16(vb + voff[db][1]);
-          return u32x4{v0[0], v0[1], v1[0], v1[1]};
-        };
+    // LDS fragments of the MFMA pairs in flight (pair i of a step uses buffer i % (LDS_AHEAD+1))
+    u32x4 kf[LDS_AHEAD + 1], vf[LDS_AHEAD + 1];
+    auto load = [&](auto ko_c, auto vo_c, int i, int buf) {
+      constexpr int KO = decltype(ko_c)::value;
+      constexpr int VO = decltype(vo_c)::value;
+      kf[buf] = lds_read_b128(koff[i] + KO);
+      const int db = i >> 1, m = i & 1;
+      const u32x2 v0 = lds_read_tr16(voff[db][0] + VO + 16 * m * ROWB);
+      const u32x2 v1 = lds_read_tr16(voff[db][1] + VO + 16 * m * ROWB);
+      vf[buf] = u32x4{v0[0], v0[1], v1[0], v1[1]};
+    };
+
+    if (wave_active) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const unsigned char* kt = cur + kb * 32 * ROWB;
-          const unsigned char* vt = vt0 + kb * 32 * ROWB;
-          const bool partial = tvlo > 32 * kb || tvhi < 32 * kb + 32;
-          if constexpr (QB == 2) {
-            // phase 1: S0 = K Q0^T
-            u32x4 kf[8];
+      for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
+      // first step's fragments: K of tile 0 half 1, V of the zeroed block
+      if (LBW_ATTN_XSTEP) {
 #pragma unroll
-            for (int s = 0; s < 8; ++s) kf[s] = *reinterpret_cast<const u32x4*>(kt + koff[s]);
-            floatx16 s0, s1;
+        for (int i = 0; i < LDS_AHEAD; ++i)
+          load(std::integral_constant<int, HALF_B>{},
+               std::integral_constant<int, (NSTAGE - 1) * TILE_B + HALF_B>{}, i, i);
+      }
+    }
+
+    // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow) into
+    // p_out, O += V^T p_in^T from LDS offset VO, s_out = K Q^T from LDS offset KO. With PRE
+    // the first LDS_AHEAD pairs' fragments were loaded by the previous step; with a nonzero
+    // next_c (NKO, NVO) this step loads the first pairs of the next step at its end (no
+    // barrier lies between them).
+    auto step = [&](auto koff_c, auto voff_c, auto pre_c, auto next_c, floatx16& s_in,
+                    floatx16& s_out, u32x4 (&p_in)[2], u32x4 (&p_out)[2], int kb, int vrow) {
+      constexpr int KO = decltype(koff_c)::value;
+      constexpr int VO = decltype(voff_c)::value;
+      constexpr bool PRE = decltype(pre_c)::value;
+      constexpr int NEXT = decltype(next_c)::value;  // NKO/HALF_B | NVO/HALF_B << 8, or -1
+      const auto ko_c = std::integral_constant<int, KO>{};
+      const auto vo_c = std::integral_constant<int, VO>{};
+      if constexpr (!PRE) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) { s0[r] = 0.0f; s1[r] = 0.0f; }
+        for (int i = 0; i < LDS_AHEAD; ++i) load(ko_c, vo_c, i, i);
+      }
+      if (pend) scale_acc(oacc, alpha_p);
+      const int vlo = vrow & 0xffff, vhi = vrow >> 16;
+      if (vlo > 32 * kb || vhi < 32 * kb + 32) mask_scores(s_in, kb, vlo, vhi, hl);
+      // softmax, part 1: running max and exponent reference (wave-uniform decision)
+      float mx = s_in[0];
 #pragma unroll
-            for (int s = 0; s < 8; ++s) s0 = mfma32x32x16(kf[s], qf[0][s], s0);
-            if (partial) mask_scores(s0, kb, tvlo, tvhi, hl);
-            // phase 2: S1 = K Q1^T  |  softmax of query block 0
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+      mx = wave_max_xor32(mx);
+      m_true = fmaxf(m_true, mx);
+      const bool move = __any(m_true > m_used + tau_raw);
+      const float m_new = move ? m_true : m_used;
+      const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2((m_used - m_new) * c);
+      m_used = m_new;
+      const float mc = m_used == -INFINITY ? 0.0f : m_used * c;
+      // MFMAs of the neighbouring sub-blocks
 #pragma unroll
-            for (int s = 0; s < 8; ++s) s1 = mfma32x32x16(kf[s], qf[QB - 1][s], s1);
-            u32x4 p0[2];
-            float alpha0;
-            const bool r0 = softmax_block(s0, m_true[0], m_used[0], lsum[0], c, tau_raw, p0, alpha0);
+      for (int r = 0; r < 16; ++r) s_out[r] = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-              __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // 8 VALU
-            }
-            if (partial) mask_scores(s1, kb, tvlo, tvhi, hl);
-            if (r0) scale_acc(oacc[0], alpha0);
-            // phase 3: O0 += V^T P0^T  |  softmax of query block 1
-            u32x4 vf[4][2];
+      for (int i = 0; i < 8; ++i) {
+        if (i + LDS_AHEAD < 8) load(ko_c, vo_c, i + LDS_AHEAD, (i + LDS_AHEAD) % (LDS_AHEAD + 1));
+        s_out = mfma32x32x16(kf[i % (LDS_AHEAD + 1)], qf[i], s_out);
+        oacc[i >> 1] = mfma32x32x16(vf[i % (LDS_AHEAD + 1)], p_in[i & 1], oacc[i >> 1]);
+      }
+      if constexpr (NEXT >= 0) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+        for (int i = 0; i < LDS_AHEAD; ++i)
+          load(std::integral_constant<int, (NEXT & 0xff) * HALF_B>{},
+               std::integral_constant<int, (NEXT >> 8) * HALF_B>{}, i, i);
+      }
+      // softmax, part 2: P = exp2(s c - m c) packed to bf16 in the PV operand order; the row
+      // sum adds the bf16 values the PV MFMAs use (v_dot2 with (1, 1), two chains)
+      #if LBW_ATTN_DOT2_SUM
+      float ls0 = 0.0f, ls1 = 0.0f;
+#else
+      float ls = 0.0f;
+#endif
 #pragma unroll
-              for (int m = 0; m < 2; ++m) vf[db][m] = vfrag(vt, db, m);
+      for (int m = 0; m < 2; ++m) {
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-              for (int m = 0; m < 2; ++m) oacc[0][db] = mfma32x32x16(vf[db][m], p0[m], oacc[0][db]);
-            u32x4 p1[2];
-            float alpha1;
-            const bool r1 = softmax_block(s1, m_true[QB - 1], m_used[QB - 1], lsum[QB - 1], c,
-                                          tau_raw, p1, alpha1);
-            __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);   // the V transpose reads first
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-              __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
-            }
-            if (r1) scale_acc(oacc[QB - 1], alpha1);
-            // phase 4: O1 += V^T P1^T
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-              for (int m = 0; m < 2; ++m)
-                oacc[QB - 1][db] = mfma32x32x16(vf[db][m], p1[m], oacc[QB - 1][db]);
-          } else {
-            // one 32-query block: S = K Q^T, softmax, O += V^T P^T (the other wave on this
-            // SIMD fills the gaps)
-            floatx16 s0;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) s0[r] = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 8; ++s)
-              s0 = mfma32x32x16(*reinterpret_cast<const u32x4*>(kt + koff[s]), qf[0][s], s0);
-            if (partial) mask_scores(s0, kb, tvlo, tvhi, hl);
-            u32x4 p0[2];
-            float alpha0;
-            const bool r0 = softmax_block(s0, m_true[0], m_used[0], lsum[0], c, tau_raw, p0, alpha0);
-            if (r0) scale_acc(oacc[0], alpha0);
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-              for (int m = 0; m < 2; ++m)
-                oacc[0][db] = mfma32x32x16(vfrag(vt, db, m), p0[m], oacc[0][db]);
-          }
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], c, -mc));
+          const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], c, -mc));
+          p_out[m][e] = pack_bf16x2(x0, x1);
+#if LBW_ATTN_DOT2_SUM
+          if (e & 1) ls1 = dot2_bf16_ones(p_out[m][e], ls1);
+          else ls0 = dot2_bf16_ones(p_out[m][e], ls0);
+#else
+          ls += x0 + x1;
+#endif
         }
       }
+#if LBW_ATTN_DOT2_SUM
+      const float ls = ls0 + ls1;
+#endif
+      lsum = __builtin_fmaf(lsum, alpha, ls);
+      // keep the exponentials in this step's block (not sunk into the next one)
+      asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
+      // schedule: the first LDS_AHEAD pairs' fragments, then per MFMA pair: MFMA, 4 VALU,
+      // MFMA, 4 VALU, the 3 LDS reads of the pair LDS_AHEAD ahead
+      if constexpr (!PRE) __builtin_amdgcn_sched_group_barrier(0x100, 3 * LDS_AHEAD, 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, LBW_ATTN_VALU_A, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, LBW_ATTN_VALU_B, 0);
+        if (i + LDS_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // 3 LDS reads
+      }
+      if constexpr (NEXT >= 0) __builtin_amdgcn_sched_group_barrier(0x100, 3 * LDS_AHEAD, 0);
+      pend = move;
+      alpha_p = alpha;
+    };
 
-      // tile t+1 must be in LDS for every wave before the next iteration
-      if (has2) wait_vmcnt_le<2 * NDMA>(); else wait_vmcnt_0();
+    // Tile u lives in stage u % NSTAGE (K at stage*16 KB, V at V_BASE + stage*16 KB).
+    // Step 2u: softmax of tile u half 0, PV of tile u-1 half 1, S of tile u half 1.
+    // Step 2u+1: softmax of tile u half 1, PV of tile u half 0, S of tile u+1 half 0.
+    // Between them: wait for tile u+1, barrier (every wave is past its reads of tile u-1),
+    // refill tile u-1's stage with tile u+NSTAGE-1.
+    auto tile = [&](auto st_c, int u) {
+      constexpr int ST = decltype(st_c)::value;
+      constexpr int SP = (ST + NSTAGE - 1) % NSTAGE;  // stage of tile u-1
+      constexpr int SN = (ST + 1) % NSTAGE;           // stage of tile u+1
+      const int vrow = vr[0];
+      if (wave_active)
+        step(std::integral_constant<int, ST * TILE_B + HALF_B>{},
+             std::integral_constant<int, SP * TILE_B + HALF_B>{},
+             std::integral_constant<bool, LBW_ATTN_XSTEP != 0>{},
+             std::integral_constant<int, -1>{}, sA, sB, pA, pB, 0, vrow);
+      if (u + 1 < T) wait_tiles_outstanding(min(NSTAGE - 3, T - 2 - u));
       barrier_nofence();
-      vlo[0] = vlo[1]; vhi[0] = vhi[1];
-      vlo[1] = vlo[2]; vhi[1] = vhi[2];
-      st = st == 2 ? 0 : st + 1;
+      if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = issue(SP);
+      // the next step (tile u+1 half 0 softmax): K of tile u+1 half 1, V of tile u half 1
+      constexpr int NEXT = LBW_ATTN_XSTEP ? (2 * SN + 1) | ((2 * ST + 1) << 8) : -1;
+      if (wave_active)
+        step(std::integral_constant<int, SN * TILE_B>{},
+             std::integral_constant<int, ST * TILE_B>{}, std::false_type{},
+             std::integral_constant<int, NEXT>{}, sB, sA, pB, pA, 1, vrow);
+#pragma unroll
+      for (int k = 0; k < NSTAGE - 1; ++k) vr[k] = vr[k + 1];
+    };
+
+#pragma unroll 1
+    for (int u = 0; u < T; u += NSTAGE) {
+      tile(std::integral_constant<int, 0>{}, u);
+      if (u + 1 < T) tile(std::integral_constant<int, 1>{}, u + 1);
+      if (u + 2 < T) tile(std::integral_constant<int, 2>{}, u + 2);
+      if constexpr (NSTAGE == 4)
+        if (u + 3 < T) tile(std::integral_constant<int, 3 % NSTAGE>{}, u + 3);
+    }
+
+    // drain: O += V^T P^T of the last sub-block (tile T-1 half 1, P in pA)
+    if (wave_active) {
+      if (pend) scale_acc(oacc, alpha_p);
+      const int vo = ((T - 1) % NSTAGE) * TILE_B + HALF_B;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int db = i >> 1, m = i & 1;
+        const u32x2 v0 = lds_read_tr16(voff[db][0] + vo + 16 * m * ROWB);
+        const u32x2 v1 = lds_read_tr16(voff[db][1] + vo + 16 * m * ROWB);
+        oacc[db] = mfma32x32x16(u32x4{v0[0], v0[1], v1[0], v1[1]}, pA[m], oacc[db]);
+      }
     }
   }
 
   if (!wave_active) return;
 
   // ---- epilogue
+  const int q = q0 + l32;
+  const float l_tot = wave_sum_xor32(lsum);
+  if (a.mode == kModeNormalized) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (q < a.Lq) {
+      uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)q + a.osh * h;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int q = q0 + 32 * qb + l32;
-    const float l_tot = wave_sum_xor32(lsum[qb]);
-    if (a.mode == kModeNormalized) {
-      const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-      if (q < a.Lq) {
-        uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)q + a.osh * h;
+      for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int d0 = 32 * db + 8 * g + 4 * hl;
-            u32x2 w;
-            w[0] = pack_bf16x2(oacc[qb][db][4 * g + 0] * inv, oacc[qb][db][4 * g + 1] * inv);
-            w[1] = pack_bf16x2(oacc[qb][db][4 * g + 2] * inv, oacc[qb][db][4 * g + 3] * inv);
-            *reinterpret_cast<u32x2*>(op + d0) = w;
-          }
-      }
-    } else {
-      // cte_partial contract: O and l relative to the true row max, m in scaled units.
-      float f = 1.0f;
-      float m_out = -INFINITY;
-      if (l_tot > 0.0f) {
-        f = fast_exp2((m_used[qb] - m_true[qb]) * c);
-        m_out = m_true[qb] * a.scale;
-      }
-      if (q < a.Lq) {
-        const int64_t row = ((int64_t)(split * a.B + b) * a.H + h) * a.Lq + q;
-        float* po = a.part_o + row * D;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int d0 = 32 * db + 8 * g + 4 * hl;
-            floatx4 w;
-            w[0] = oacc[qb][db][4 * g + 0] * f;
-            w[1] = oacc[qb][db][4 * g + 1] * f;
-            w[2] = oacc[qb][db][4 * g + 2] * f;
-            w[3] = oacc[qb][db][4 * g + 3] * f;
-            *reinterpret_cast<floatx4*>(po + d0) = w;
-          }
-        if (hl == 0) {
-          a.part_m[row] = m_out;
-          a.part_l[row] = l_tot * f;
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * db + 8 * g + 4 * hl;
+          u32x2 w;
+          w[0] = pack_bf16x2(oacc[db][4 * g + 0] * inv, oacc[db][4 * g + 1] * inv);
+          w[1] = pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
+          *reinterpret_cast<u32x2*>(op + d0) = w;
         }
+    }
+  } else {
+    // cte_partial contract: O and l relative to the true row max, m in scaled units.
+    float f = 1.0f;
+    float m_out = -INFINITY;
+    if (l_tot > 0.0f) {
+      f = fast_exp2((m_used - m_true) * c);
+      m_out = m_true * a.scale;
+    }
+    if (q < a.Lq) {
+      const int64_t row = ((int64_t)(split * a.B + b) * a.H + h) * a.Lq + q;
+      float* po = a.part_o + row * D;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 32 * db + 8 * g + 4 * hl;
+          floatx4 w;
+          w[0] = oacc[db][4 * g + 0] * f;
+          w[1] = oacc[db][4 * g + 1] * f;
+          w[2] = oacc[db][4 * g + 2] * f;
+          w[3] = oacc[db][4 * g + 3] * f;
+          *reinterpret_cast<floatx4*>(po + d0) = w;
+        }
+      if (hl == 0) {
+        a.part_m[row] = m_out;
+        a.part_l[row] = l_tot * f;
       }
     }
   }
@@ -428,22 +522,13 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-template <int NW>
-static hipError_t launch_nw(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<NW>,
+hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t nwg = (uint32_t)a.n_qtiles * a.splits * a.H * a.B;
-  hipLaunchKernelGGL(attn_fwd_bf16_kernel<NW>, dim3(nwg), dim3(NW * 64), LDS_B, stream, a);
+  hipLaunchKernelGGL(attn_fwd_bf16_kernel, dim3(nwg), dim3(NWAVE * 64), LDS_B, stream, a);
   return hipGetLastError();
-}
-
-#ifndef LBW_ATTN_WAVES
-#define LBW_ATTN_WAVES 8
-#endif
-
-hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
-  return launch_nw<LBW_ATTN_WAVES>(a, stream);
 }
 
 }  // namespace lbw
