@@ -6,8 +6,12 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+#include <functional>
 #include <mutex>
+#include <queue>
 #include <string>
+#include <vector>
 
 #include "lbw_attn.h"
 #include "attn_fwd.h"
@@ -49,6 +53,63 @@ int num_cus() {
     cache[dev] = n;
   }
   return cache[dev];
+}
+
+// Estimated run time, in tile steps, of a launch with s KV splits: greedy list scheduling of
+// the workgroups in dispatch order (q-tile fastest, then split, then batch x head) over the
+// CUs, one workgroup per CU. A workgroup costs its tile count times (0.3 + 0.7 * its share of
+// active query waves); each split beyond the first adds 3 % (partials written and merged).
+// The constants are fitted to measured gfx950 times of the 1.3B/14B chunk shapes.
+double split_cost(int64_t bh, int lq, int bm, int64_t ntiles, int s, int cus) {
+  const int nq = (lq + bm - 1) / bm;
+  const int tail_q = lq - (nq - 1) * bm;                  // queries in the last q-tile
+  const double tail_w = (double)((tail_q + 31) / 32) / (bm / 32);
+  const int64_t per = (ntiles + s - 1) / s;
+  std::priority_queue<double, std::vector<double>, std::greater<double>> cu;
+  for (int i = 0; i < cus; ++i) cu.push(0.0);
+  for (int64_t g = 0; g < bh; ++g)
+    for (int sp = 0; sp < s; ++sp) {
+      const int64_t t0 = sp * per, t1 = std::min<int64_t>(ntiles, t0 + per);
+      const double tiles = t1 > t0 ? (double)(t1 - t0) : 0.0;
+      for (int qt = 0; qt < nq; ++qt) {
+        const double w = qt + 1 < nq ? 1.0 : tail_w;
+        const double t = cu.top();
+        cu.pop();
+        cu.push(t + tiles * (0.3 + 0.7 * w));
+      }
+    }
+  double span = 0.0;
+  while (!cu.empty()) { span = cu.top(); cu.pop(); }
+  return span * (1.0 + 0.03 * (s - 1));
+}
+
+// Number of KV splits (1..8) with the lowest estimated time; decisions are cached per shape.
+int choose_splits(int64_t bh, int lq, int bm, int64_t ntiles, int cus) {
+  struct Entry { int64_t bh, ntiles; int lq, cus, splits; };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int n_cached = 0, next = 0;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    for (int i = 0; i < n_cached; ++i) {
+      const Entry& e = cache[i];
+      if (e.bh == bh && e.ntiles == ntiles && e.lq == lq && e.cus == cus) return e.splits;
+    }
+  }
+  int best_s = 1;
+  const int64_t nq = (lq + bm - 1) / bm;
+  if (bh * nq * 8 <= 200000) {  // keep the simulation cheap; huge launches need no split
+    double best = split_cost(bh, lq, bm, ntiles, 1, cus);
+    for (int s = 2; s <= 8 && ntiles / s >= 8; ++s) {
+      const double c = split_cost(bh, lq, bm, ntiles, s, cus);
+      if (c < best) { best = c; best_s = s; }
+    }
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  cache[next] = Entry{bh, ntiles, lq, cus, best_s};
+  next = (next + 1) % 64;
+  if (n_cached < 64) ++n_cached;
+  return best_s;
 }
 
 struct Plan {
@@ -142,17 +203,8 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
     if (p->num_splits > 0) {
       splits = p->num_splits > 16 ? 16 : p->num_splits;
     } else {
-      const int64_t base = (int64_t)a.n_qtiles * a.H * a.B;
       const int64_t ntiles = (a.hi - a.lo + bn - 1) / bn;
-      const int cus = num_cus();
-      double best = 0.0;
-      for (int s = 1; s <= 8; ++s) {
-        if (s > 1 && ntiles / s < 8) break;
-        const int64_t n = base * s;
-        const int64_t rounds = (n + cus - 1) / cus;
-        const double eff = (double)n / (double)(rounds * cus);
-        if (eff > best * 1.03) { best = eff; splits = s; }
-      }
+      splits = choose_splits((int64_t)a.H * a.B, p->lq, bm, ntiles, num_cus());
     }
   }
   plan->splits = splits;

@@ -78,3 +78,35 @@ def test_entry_points_reject_bad_arguments_without_gpu():
     assert lib.lbw_attention_fwd(ctypes.byref(p), None, 0, None) == 1
     assert lib.lbw_attention_workspace_size(ctypes.byref(p)) == 0
     assert lib.lbw_kv_quant_fp8(None, 1, 10, 1, 128, 0, 0, 0, None, None, 32, None) == 2
+
+
+def _split_count(H, LQ, LK):
+    """KV splits the library plans for q [1, LQ, H, 128] over one LK-key segment, read back
+    from the workspace size (splits x rows x (D + 2) fp32; 0 for a single pass). Host-only."""
+    from lbw_amd import _lib
+    lib = _lib.load()
+    p = _lib.AttnParams()
+    p.batch, p.heads, p.head_dim, p.lq = 1, H, 128, LQ
+    p.q = p.out = 256
+    p.q_stride_b = p.o_stride_b = LQ * H * 128
+    p.q_stride_l = p.o_stride_l = H * 128
+    p.q_stride_h = p.o_stride_h = 128
+    p.n_segments = 1
+    s = p.seg[0]
+    s.k = s.v = 256
+    s.len = LK
+    s.k_stride_b = s.v_stride_b = LK * H * 128
+    s.k_stride_l = s.v_stride_l = H * 128
+    s.k_stride_h = s.v_stride_h = 128
+    p.kv_lo, p.kv_hi = 0, -1
+    n = lib.lbw_attention_workspace_size(ctypes.byref(p))
+    return n // (LQ * H * 130 * 4)
+
+
+def test_split_plan_for_the_measured_shapes():
+    """The split heuristic's choices for the shapes it was fitted on (gfx950, 256 CUs): 14B
+    720p (3 splits), 14B 480p and 1.3B 480p 3-frame chunks (single pass), 1.3B one frame (3)."""
+    assert _split_count(40, 3600, 46800) == 3
+    assert _split_count(40, 4680, 32760) == 0
+    assert _split_count(12, 4680, 14040) == 0
+    assert _split_count(12, 1560, 4680) == 3
