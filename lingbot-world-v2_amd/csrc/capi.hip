@@ -322,9 +322,10 @@ int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream) {
   if (p->tokens < 0 || p->heads < 1 || p->dim < 8 || p->dim % p->heads != 0)
     return fail(LBW_ERR_INVALID, "bad sizes tokens=%d dim=%d heads=%d", p->tokens, p->dim, p->heads);
   const int D = p->dim / p->heads;
-  if (D % 8 != 0 || p->dim % 8 != 0 || p->dim > 8192)
-    return fail(LBW_ERR_UNSUPPORTED, "dim %d / head_dim %d: need multiples of 8, dim <= 8192",
-                p->dim, D);
+  if (D % 8 != 0 || 512 % D != 0 || p->dim % 8 != 0 || p->dim > 8192)
+    return fail(LBW_ERR_UNSUPPORTED,
+                "dim %d / head_dim %d: need head_dim a power of two in [8, 512], dim a multiple "
+                "of 8 and <= 8192", p->dim, D);
   if (p->s0 < 0 || p->s1 < 0 || p->s0 + 2 * p->s1 != D / 2)
     return fail(LBW_ERR_INVALID, "rope split s0=%d s1=%d does not cover head_dim/2=%d", p->s0,
                 p->s1, D / 2);

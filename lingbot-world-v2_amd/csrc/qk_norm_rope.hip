@@ -7,11 +7,14 @@
 //   out = bf16(rot * out_scale).
 // RoPE angles follow wan/modules/model_fast.py:878-931: token (fi, hi, wi) of the
 // frame-major grid takes pair j's cos/sin from the frame table (j < s0), the height table
-// (j < s0 + s1) or the width table. The per-axis tables live in LDS; tokens past f*h*w are
-// not rotated (model_fast.py:972-975).
+// (j < s0 + s1) or the width table. Tokens past f*h*w are not rotated (model_fast.py:972-975).
 //
-// One wave per token row: 64 lanes x 16-byte chunks, the row held in registers between the
-// reduction and the write-back (C <= 8192), the reduction done with cross-lane shuffles.
+// HBM-bound: per token the kernel reads q, k (and v) rows and writes q', k' (and v). One wave
+// per token row; lane l holds the 16-byte chunks l, l + 64, ... of the row (NCH of them), so
+// with the head dim dividing 512 every chunk of a lane covers the same 4 rotation pairs and the
+// lane fetches its 4 cos/sin pairs once per row (shared by q and k). The q and k rows are
+// loaded together before any arithmetic, so each wave keeps two rows of loads in flight; the
+// per-axis RoPE tables and the bias / gamma vectors sit in LDS.
 
 #include "common.h"
 #include "attn_fwd.h"
@@ -19,141 +22,229 @@
 namespace lbw {
 
 constexpr int QK_WAVES = 4;
-constexpr int QK_MAX_CHUNKS = 16;          // chunks of 8 per lane: C <= 16 * 64 * 8 = 8192
+constexpr int QK_MAX_NCH = 16;             // chunks of 8 per lane: C <= 16 * 64 * 8 = 8192
 constexpr int QK_MAX_TABLE = 16384;        // floats of per-axis tables held in LDS (64 KB)
 
 int qk_norm_rope_max_table_floats() { return QK_MAX_TABLE; }
 
-struct RopePair {
-  float c[4];
-  float s[4];
-};
-
-__device__ __forceinline__ void rope_lookup(const float* tab, const QkNormRopeArgs& a, int fi,
-                                            int hi, int wi, int j0, RopePair& rp) {
-  const int base_h = 2 * a.gf * a.s0;
-  const int base_w = base_h + 2 * a.gh * a.s1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int j = j0 + i;
-    int ci, si;
-    if (j < a.s0) {
-      ci = fi * a.s0 + j;
-      si = ci + a.gf * a.s0;
-    } else if (j < a.s0 + a.s1) {
-      ci = base_h + hi * a.s1 + (j - a.s0);
-      si = ci + a.gh * a.s1;
-    } else {
-      ci = base_w + wi * a.s1 + (j - a.s0 - a.s1);
-      si = ci + a.gw * a.s1;
-    }
-    rp.c[i] = tab[ci];
-    rp.s[i] = tab[si];
-  }
+// LDS layout: [ntab floats of tables][bq | bk | gq | gk as bf16, C each]
+__host__ __device__ inline int qk_table_floats(int ntab) { return (ntab + 3) & ~3; }
+__host__ __device__ inline size_t qk_lds_bytes(int ntab, int C) {
+  return (size_t)qk_table_floats(ntab) * 4 + (size_t)4 * C * 2;
 }
 
-// Process one [C] row: x (+bias) -> norm -> gamma -> rope -> out.
-__device__ __forceinline__ void norm_rope_row(const QkNormRopeArgs& a, const float* tab,
-                                              const uint16_t* x, const uint16_t* bias,
-                                              const uint16_t* gamma, uint16_t* out,
-                                              float out_scale, bool rotate, int fi, int hi,
-                                              int wi, int lane) {
-  const int nchunk = a.C / 8;
-  float y[QK_MAX_CHUNKS][8];
-  float ss = 0.0f;
+template <int NCH>
+__global__ void __launch_bounds__(QK_WAVES * 64)
+qk_norm_rope_kernel(const QkNormRopeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int C = a.C;
+  const int nchunk = C / 8;
+  float* tab = smem;
+  uint16_t* vec = reinterpret_cast<uint16_t*>(smem + qk_table_floats(a.ntab));
+  {
+    // tables and vectors into LDS, several loads in flight per thread (unrolled by 4)
+    const int nt2 = a.ntab / 2;  // cos/sin values come in pairs: 8-byte loads
+#pragma unroll 4
+    for (int i = threadIdx.x; i < nt2; i += blockDim.x)
+      reinterpret_cast<u32x2*>(tab)[i] = reinterpret_cast<const u32x2*>(a.rope)[i];
+    const uint16_t* src[4] = {a.bq, a.bk, a.wq, a.wk};
 #pragma unroll
-  for (int i = 0; i < QK_MAX_CHUNKS; ++i) {
-    const int ch = lane + 64 * i;
-    if (ch < nchunk) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(x + 8 * ch);
-      u32x4 bv = {0u, 0u, 0u, 0u};
-      if (bias != nullptr) bv = *reinterpret_cast<const u32x4*>(bias + 8 * ch);
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        y[i][2 * w] = __fadd_rn(bf16_lo(v[w]), bf16_lo(bv[w]));
-        y[i][2 * w + 1] = __fadd_rn(bf16_hi(v[w]), bf16_hi(bv[w]));
+    for (int v = 0; v < 4; ++v) {
+      if (src[v] != nullptr) {
+#pragma unroll 4
+        for (int ch = threadIdx.x; ch < nchunk; ch += blockDim.x)
+          *reinterpret_cast<u32x4*>(vec + v * C + 8 * ch) =
+              *reinterpret_cast<const u32x4*>(src[v] + 8 * ch);
+      } else {
+        for (int ch = threadIdx.x; ch < nchunk; ch += blockDim.x)
+          *reinterpret_cast<u32x4*>(vec + v * C + 8 * ch) = u32x4{0u, 0u, 0u, 0u};
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __fmaf_rn(y[i][e], y[i][e], ss);
     }
   }
-  ss = wave_reduce_sum(ss);
-  const float r = 1.0f / sqrtf(__fadd_rn(__fmul_rn(ss, a.inv_c), a.eps));
-  const int D = a.C / a.H;
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int D = C / a.H;
+  const int j0 = ((8 * lane) % D) / 2;  // first rotation pair of every chunk of this lane
+  const int grid_tokens = a.gf * a.gh * a.gw;
+  const int base_h = 2 * a.gf * a.s0;
+  const int base_w = base_h + 2 * a.gh * a.s1;
+
+  for (int row = blockIdx.x * QK_WAVES + wave; row < a.L; row += gridDim.x * QK_WAVES) {
+    // ---- loads: q and k rows together, then v if it is copied
+    u32x4 xq[NCH], xk[NCH];
+    const uint16_t* qr = a.q + a.qs * row;
+    const uint16_t* kr = a.k + a.ks * row;
 #pragma unroll
-  for (int i = 0; i < QK_MAX_CHUNKS; ++i) {
-    const int ch = lane + 64 * i;
-    if (ch < nchunk) {
-      const u32x4 gv = *reinterpret_cast<const u32x4*>(gamma + 8 * ch);
+    for (int i = 0; i < NCH; ++i) {
+      const int ch = lane + 64 * i;
+      if (i + 1 < NCH || ch < nchunk) {  // only the last chunk can run past the row
+        xq[i] = *reinterpret_cast<const u32x4*>(qr + 8 * ch);
+        xk[i] = *reinterpret_cast<const u32x4*>(kr + 8 * ch);
+      }
+    }
+
+    // ---- this lane's 4 rotation pairs for the row's (frame, row, column)
+    const bool rotate = row < grid_tokens;
+    float cr[4], sr[4];
+    if (rotate) {
+      const int wi = row % a.gw;
+      const int hi = (row / a.gw) % a.gh;
+      const int fi = row / (a.gw * a.gh);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int j = j0 + p;
+        int ci, si;
+        if (j < a.s0) {
+          ci = fi * a.s0 + j;
+          si = ci + a.gf * a.s0;
+        } else if (j < a.s0 + a.s1) {
+          ci = base_h + hi * a.s1 + (j - a.s0);
+          si = ci + a.gh * a.s1;
+        } else {
+          ci = base_w + wi * a.s1 + (j - a.s0 - a.s1);
+          si = ci + a.gw * a.s1;
+        }
+        cr[p] = tab[ci];
+        sr[p] = tab[si];
+      }
+    }
+
+    // ---- sums of squares of y = x + b (per lane in chunk order, then across the wave)
+    float ssq = 0.0f, ssk = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ch = lane + 64 * i;
+      if (i + 1 < NCH || ch < nchunk) {
+        const u32x4 bq = *reinterpret_cast<const u32x4*>(vec + 8 * ch);
+        const u32x4 bk = *reinterpret_cast<const u32x4*>(vec + C + 8 * ch);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float q0 = __fadd_rn(bf16_lo(xq[i][w]), bf16_lo(bq[w]));
+          const float q1 = __fadd_rn(bf16_hi(xq[i][w]), bf16_hi(bq[w]));
+          const float k0 = __fadd_rn(bf16_lo(xk[i][w]), bf16_lo(bk[w]));
+          const float k1 = __fadd_rn(bf16_hi(xk[i][w]), bf16_hi(bk[w]));
+          ssq = __fmaf_rn(q0, q0, ssq);
+          ssq = __fmaf_rn(q1, q1, ssq);
+          ssk = __fmaf_rn(k0, k0, ssk);
+          ssk = __fmaf_rn(k1, k1, ssk);
+        }
+      }
+    }
+    ssq = wave_reduce_sum(ssq);
+    ssk = wave_reduce_sum(ssk);
+    const float rq = 1.0f / sqrtf(__fadd_rn(__fmul_rn(ssq, a.inv_c), a.eps));
+    const float rk = 1.0f / sqrtf(__fadd_rn(__fmul_rn(ssk, a.inv_c), a.eps));
+
+    // ---- normalise, gamma, rotate, store
+    auto finish = [&](const u32x4& x, const u32x4& bv, const u32x4& gv, float r, float scale,
+                      uint16_t* dst) {
       float t[8];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        t[2 * w] = __fmul_rn(round_bf16(__fmul_rn(y[i][2 * w], r)), bf16_lo(gv[w]));
-        t[2 * w + 1] = __fmul_rn(round_bf16(__fmul_rn(y[i][2 * w + 1], r)), bf16_hi(gv[w]));
+        const float y0 = __fadd_rn(bf16_lo(x[w]), bf16_lo(bv[w]));
+        const float y1 = __fadd_rn(bf16_hi(x[w]), bf16_hi(bv[w]));
+        t[2 * w] = __fmul_rn(round_bf16(__fmul_rn(y0, r)), bf16_lo(gv[w]));
+        t[2 * w + 1] = __fmul_rn(round_bf16(__fmul_rn(y1, r)), bf16_hi(gv[w]));
       }
       float o[8];
       if (rotate) {
-        const int j0 = ((8 * ch) % D) / 2;
-        RopePair rp;
-        rope_lookup(tab, a, fi, hi, wi, j0, rp);
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const float re = t[2 * p], im = t[2 * p + 1];
-          o[2 * p] = __fsub_rn(__fmul_rn(re, rp.c[p]), __fmul_rn(im, rp.s[p]));
-          o[2 * p + 1] = __fadd_rn(__fmul_rn(re, rp.s[p]), __fmul_rn(im, rp.c[p]));
+          o[2 * p] = __fsub_rn(__fmul_rn(re, cr[p]), __fmul_rn(im, sr[p]));
+          o[2 * p + 1] = __fadd_rn(__fmul_rn(re, sr[p]), __fmul_rn(im, cr[p]));
         }
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = t[e];
       }
-      if (out_scale != 1.0f) {
+      if (scale != 1.0f) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = __fmul_rn(o[e], out_scale);
+        for (int e = 0; e < 8; ++e) o[e] = __fmul_rn(o[e], scale);
       }
       u32x4 ov;
 #pragma unroll
       for (int w = 0; w < 4; ++w) ov[w] = pack_bf16x2(o[2 * w], o[2 * w + 1]);
-      *reinterpret_cast<u32x4*>(out + 8 * ch) = ov;
+      *reinterpret_cast<u32x4*>(dst) = ov;
+    };
+    uint16_t* qo = a.qo + a.qos * row;
+    uint16_t* ko = a.ko + a.kos * row;
+    // recompute y = x + b below (bias re-read from LDS) rather than keeping the fp32 values
+    // and bias chunks of the first pass alive
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      asm volatile("" : "+v"(xq[i]));
+      asm volatile("" : "+v"(xk[i]));
     }
-  }
-}
-
-__global__ void __launch_bounds__(QK_WAVES * 64)
-qk_norm_rope_kernel(const QkNormRopeArgs a) {
-  __shared__ float tab[QK_MAX_TABLE];
-  for (int i = threadIdx.x; i < a.ntab; i += blockDim.x) tab[i] = a.rope[i];
-  __syncthreads();
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int grid_tokens = a.gf * a.gh * a.gw;
-  for (int row = blockIdx.x * QK_WAVES + wave; row < a.L; row += gridDim.x * QK_WAVES) {
-    const bool rotate = row < grid_tokens;
-    int fi = 0, hi = 0, wi = 0;
-    if (rotate) {
-      wi = row % a.gw;
-      hi = (row / a.gw) % a.gh;
-      fi = row / (a.gw * a.gh);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int ch = lane + 64 * i;
+      if (i + 1 < NCH || ch < nchunk) {
+        finish(xq[i], *reinterpret_cast<const u32x4*>(vec + 8 * ch),
+               *reinterpret_cast<const u32x4*>(vec + 2 * C + 8 * ch), rq, a.q_scale, qo + 8 * ch);
+        finish(xk[i], *reinterpret_cast<const u32x4*>(vec + C + 8 * ch),
+               *reinterpret_cast<const u32x4*>(vec + 3 * C + 8 * ch), rk, a.k_scale, ko + 8 * ch);
+      }
     }
-    norm_rope_row(a, tab, a.q + a.qs * row, a.bq, a.wq, a.qo + a.qos * row, a.q_scale, rotate,
-                  fi, hi, wi, lane);
-    norm_rope_row(a, tab, a.k + a.ks * row, a.bk, a.wk, a.ko + a.kos * row, a.k_scale, rotate,
-                  fi, hi, wi, lane);
+
+    // ---- V copy into its cache slot
     if (a.v != nullptr) {
       const uint16_t* vs = a.v + a.vs * row;
       uint16_t* vd = a.vo + a.vos * row;
-      for (int ch = lane; ch < a.C / 8; ch += 64)
-        *reinterpret_cast<u32x4*>(vd + 8 * ch) = *reinterpret_cast<const u32x4*>(vs + 8 * ch);
+      u32x4 xv[NCH];
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int ch = lane + 64 * i;
+        if (i + 1 < NCH || ch < nchunk) xv[i] = *reinterpret_cast<const u32x4*>(vs + 8 * ch);
+      }
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int ch = lane + 64 * i;
+        if (i + 1 < NCH || ch < nchunk) *reinterpret_cast<u32x4*>(vd + 8 * ch) = xv[i];
+      }
     }
   }
 }
 
-hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, hipStream_t stream) {
+template <int NCH>
+static hipError_t launch_nch(const QkNormRopeArgs& a, hipStream_t stream) {
+  static hipError_t attr = hipFuncSetAttribute((const void*)qk_norm_rope_kernel<NCH>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)qk_lds_bytes(QK_MAX_TABLE, 64 * 8 * NCH));
+  if (attr != hipSuccess) return attr;
+  // about two workgroups per CU, each wave looping over rows (the LDS fill is paid once)
   int blocks = (a.L + QK_WAVES - 1) / QK_WAVES;
-  if (blocks > 1024) blocks = 1024;
+  if (blocks > 512) blocks = 512;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(blocks), dim3(QK_WAVES * 64), 0, stream, a);
+  hipLaunchKernelGGL(qk_norm_rope_kernel<NCH>, dim3(blocks), dim3(QK_WAVES * 64),
+                     qk_lds_bytes(a.ntab, a.C), stream, a);
   return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, hipStream_t stream) {
+  const int nch = (a.C / 8 + 63) / 64;
+  switch (nch) {
+    case 1: return launch_nch<1>(a, stream);
+    case 2: return launch_nch<2>(a, stream);
+    case 3: return launch_nch<3>(a, stream);
+    case 4: return launch_nch<4>(a, stream);
+    case 5: return launch_nch<5>(a, stream);
+    case 6: return launch_nch<6>(a, stream);
+    case 7: return launch_nch<7>(a, stream);
+    case 8: return launch_nch<8>(a, stream);
+    case 9: return launch_nch<9>(a, stream);
+    case 10: return launch_nch<10>(a, stream);
+    case 11: return launch_nch<11>(a, stream);
+    case 12: return launch_nch<12>(a, stream);
+    case 13: return launch_nch<13>(a, stream);
+    case 14: return launch_nch<14>(a, stream);
+    case 15: return launch_nch<15>(a, stream);
+    case 16: return launch_nch<16>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace lbw
