@@ -215,9 +215,10 @@ static hipError_t launch_nch(const QkNormRopeArgs& a, hipStream_t stream) {
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                (int)qk_lds_bytes(QK_MAX_TABLE, 64 * 8 * NCH));
   if (attr != hipSuccess) return attr;
-  // about two workgroups per CU, each wave looping over rows (the LDS fill is paid once)
+  // at most 1024 workgroups (two resident per CU by LDS, the rest queued), each wave looping
+  // over rows so that the LDS fill is amortised
   int blocks = (a.L + QK_WAVES - 1) / QK_WAVES;
-  if (blocks > 512) blocks = 512;
+  if (blocks > 1024) blocks = 1024;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(qk_norm_rope_kernel<NCH>, dim3(blocks), dim3(QK_WAVES * 64),
                      qk_lds_bytes(a.ntab, a.C), stream, a);
