@@ -124,6 +124,65 @@ def cpu_baseline(budget_s: float = 12.0):
                       f"ms per 40-layer chunk extrapolated: {dt / heads * H * 40 * 1e3:.0f}"}
 
 
+def _time_ms(fn, iters=10, warmup=2):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def other_configs(dev):
+    """The other workload shapes of this path, timed once each after the headline step (not
+    part of `value`): 1.3B 480p 3-frame chunk over 6 cached frames, 14B 480p 3-frame chunk over
+    18 cached frames, its cross-attention to a 512-token context (300 valid), and the 14B 720p
+    long-horizon chunk over an fp8-e4m3 cache of 24 frames + the chunk."""
+    import torch
+    from lbw_amd import attention_fp8kv, attention_segments, cross_attention, quantize_kv_fp8
+    g = torch.Generator(device=dev).manual_seed(99)
+    rnd = lambda *s: torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)
+    out = {}
+    for name, h, lq, lc in (("wan13b_480p_3f_over_6f", 12, 4680, 9360),
+                            ("wan14b_480p_3f_over_18f", 40, 4680, 28080)):
+        q = rnd(1, lq, h, D)
+        kc, vc, kn, vn = rnd(1, lc, h, D), rnd(1, lc, h, D), rnd(1, lq, h, D), rnd(1, lq, h, D)
+        ms = _time_ms(lambda: attention_segments(q, [(kc, vc), (kn, vn)]))
+        fl = 4.0 * lq * (lc + lq) * D * h
+        out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
+                     "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2)}
+        del q, kc, vc, kn, vn
+    q = rnd(1, 4680, 40, D)
+    kx, vx = rnd(1, 512, 40, D), rnd(1, 512, 40, D)
+    kl = torch.tensor([300], dtype=torch.int32, device=dev)
+    for name, lens, nk in (("wan14b_480p_cross_512ctx_300valid", kl, 300),
+                           ("wan14b_480p_cross_512ctx_unmasked", None, 512)):
+        ms = _time_ms(lambda: cross_attention(q, kx, vx, k_lens=lens), iters=20)
+        fl = 4.0 * 4680 * nk * D * 40
+        by = 2.0 * (2 * 4680 + 2 * nk) * 40 * D
+        out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
+                     "GB/s": round(by / ms / 1e6, 1),
+                     "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2),
+                     "pct_hbm_peak": round(by / ms / 1e6 / PEAK_HBM_GBS * 100, 2)}
+    del q, kx, vx
+    q = rnd(1, 3600, 40, D)
+    lk = 3600 * 25
+    k8 = quantize_kv_fp8(rnd(1, lk, 40, D))
+    v8 = quantize_kv_fp8(rnd(1, lk, 40, D))
+    ms = _time_ms(lambda: attention_fp8kv(q, [(k8, v8)]))
+    fl = 4.0 * 3600 * lk * D * 40
+    out["wan14b_720p_1f_over_24f_fp8kv"] = {
+        "ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
+        "pct_fp8_peak": round(fl / ms / 1e9 / PEAK_FP8_TFLOPS * 100, 2),
+        "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2)}
+    return out
+
+
 def pmc_workload():
     """The program the --pmc passes profile: 3 layers' qk-norm/RoPE + attention calls of the
     workload, then 3 plain copies of COPY_BYTES (calibration of the byte counters)."""
@@ -221,6 +280,8 @@ def main():
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the timings of the other workload shapes")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the program profiled by the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -311,6 +372,10 @@ def main():
                                   "frac": round(qk_bytes() / (qk_ms / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
                                   "traffic": round(tr["qk_traffic_bytes"]) if tr else None},
     }
+    if not args.no_extra:
+        del layers
+        torch.cuda.empty_cache()
+        res["other_configs"] = other_configs(dev)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(res))
