@@ -42,36 +42,17 @@
 namespace lbw {
 namespace {
 
-#ifndef LBW_ATTN_NSTAGE
-#define LBW_ATTN_NSTAGE 3
-#endif
-#ifndef LBW_ATTN_LDS_AHEAD
-#define LBW_ATTN_LDS_AHEAD 2
-#endif
-#ifndef LBW_ATTN_VALU_A
-#define LBW_ATTN_VALU_A 4
-#endif
-#ifndef LBW_ATTN_VALU_B
-#define LBW_ATTN_VALU_B 4
-#endif
-#ifndef LBW_ATTN_XSTEP
-#define LBW_ATTN_XSTEP 0
-#endif
-#ifndef LBW_ATTN_DOT2_SUM
-#define LBW_ATTN_DOT2_SUM 0
-#endif
 
 constexpr int NWAVE = 8;                // waves per workgroup (32 queries each)
 constexpr int BM = 32 * NWAVE;          // queries per workgroup
 constexpr int ROWB = D * 2;             // bytes per K/V row in LDS
 constexpr int TILE_B = BN * ROWB;       // 16 KB
 constexpr int HALF_B = TILE_B / 2;      // one 32-key sub-block
-constexpr int NSTAGE = LBW_ATTN_NSTAGE; // tiles resident or in flight
+constexpr int NSTAGE = 3;               // tiles resident or in flight
 constexpr int V_BASE = 65536;           // V tiles start here; K tiles at NSTAGE * 16 KB below
 constexpr int LDS_B = V_BASE + NSTAGE * TILE_B;
 constexpr int NDMA = TILE_B / (NWAVE * 64 * 16);  // 16-byte DMA blocks per lane per K/V tile
-constexpr int LDS_AHEAD = LBW_ATTN_LDS_AHEAD;     // MFMA pairs of LDS fragments in flight
-static_assert(NSTAGE >= 3 && NSTAGE <= 4, "LDS stages");
+constexpr int LDS_AHEAD = 2;                      // MFMA pairs of LDS fragments in flight
 static_assert(NSTAGE * TILE_B <= V_BASE, "K tiles must fit below the V tiles");
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
@@ -129,12 +110,6 @@ __device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int 
   }
 }
 
-// acc + lo(p) + hi(p) for a packed bf16 pair (v_dot2c_f32_bf16 against (1.0, 1.0)).
-__device__ __forceinline__ float dot2_bf16_ones(uint32_t p, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p),
-                                         __builtin_bit_cast(bf16x2, 0x3F803F80u), acc, false);
-}
-
 __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
 #pragma unroll
   for (int db = 0; db < 4; ++db)
@@ -142,8 +117,15 @@ __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
     for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
 }
 
+// FP8 = false: bf16 K/V, DMA'd straight into LDS. FP8 = true: e4m3 K/V codes with fp32 scales
+// per (batch, head, 64-token block): each tile is loaded into registers one tile ahead,
+// converted exactly to bf16 (every e4m3 value is a bf16 value) and written into the same LDS
+// layout; the block scales fold into the softmax (K's into the exponent's multiplier, V's into
+// its addend as log2, and out of the row sum), so the MFMA loop is the bf16 one.
+template <bool FP8>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
+  constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -267,20 +249,68 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         dma16(vb, (uint32_t)(r * cs.vs) + dma_col[i], vdst + 1024 * i);
       }
     }
-    if (cursor_next<2>(a, lo, hi, b, h, cs) && cs.seg < a.nseg) seg_offsets();
+    if (cursor_next<ESZ>(a, lo, hi, b, h, cs) && cs.seg < a.nseg) seg_offsets();
     return tvlo | (tvhi << 16);
+  };
+
+  // fp8: thread t stages row t/8, 16-byte code chunk t%8 (bf16 logical chunks 2(t%8), +1) of
+  // the K and V tiles; loads go to registers (k8, v8) and scales to sk_n / sv_n.
+  const int row8 = threadIdx.x >> 3, j8 = threadIdx.x & 7;
+  u32x4 k8 = {0u, 0u, 0u, 0u}, v8 = {0u, 0u, 0u, 0u};
+  float sk_n = 1.0f, sv_n = 1.0f;
+  auto issue8 = [&]() -> int {
+    int tvlo, tvhi;
+    cursor_rows(cs, tvlo, tvhi);
+    const int64_t row0 = cs.lt * BN;
+    int r = row8;
+    r = r < tvlo ? tvlo : (r > tvhi - 1 ? tvhi - 1 : r);
+    k8 = *reinterpret_cast<const u32x4*>(cs.kbase + (row0 + r) * cs.ks + 16 * j8);
+    v8 = *reinterpret_cast<const u32x4*>(cs.vbase + (row0 + r) * cs.vs + 16 * j8);
+    sk_n = cs.ksc[cs.lt];
+    sv_n = cs.vsc[cs.lt];
+    cursor_next<1>(a, lo, hi, b, h, cs);
+    return tvlo | (tvhi << 16);
+  };
+  auto write8 = [&](int stage) {
+    auto cvt = [](const u32x4& x, int half) {
+      const uint32_t w0 = x[2 * half], w1 = x[2 * half + 1];
+      return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+    };
+    unsigned char* kd = lds + stage * TILE_B + row8 * ROWB;
+    unsigned char* vd = kd + V_BASE;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int pc = ((2 * j8 + hf) ^ swz(row8)) << 4;
+      *reinterpret_cast<u32x4*>(kd + pc) = cvt(k8, hf);
+      *reinterpret_cast<u32x4*>(vd + pc) = cvt(v8, hf);
+    }
   };
 
   const int T = t1 - t0;
   if (T > 0) {
     int vr[NSTAGE];  // valid rows of tiles u .. u+NSTAGE-1 (u = the tile being softmaxed)
+    float skr[NSTAGE], svr[NSTAGE];  // fp8 block scales of the same tiles
 #pragma unroll
-    for (int k = 0; k < NSTAGE; ++k) vr[k] = BN << 16;
-    cursor_init<2>(a, lo, hi, t0, b, h, cs);
-    seg_offsets();
+    for (int k = 0; k < NSTAGE; ++k) { vr[k] = BN << 16; skr[k] = 1.0f; svr[k] = 1.0f; }
+    cursor_init<ESZ>(a, lo, hi, t0, b, h, cs);
+    if constexpr (FP8) {
 #pragma unroll
-    for (int k = 0; k < NSTAGE - 1; ++k)
-      if (k < T) vr[k] = issue(k);
+      for (int k = 0; k < NSTAGE - 1; ++k)
+        if (k < T) {
+          vr[k] = issue8();
+          skr[k] = sk_n;
+          svr[k] = sv_n;
+          write8(k);
+        }
+    } else {
+      seg_offsets();
+#pragma unroll
+      for (int k = 0; k < NSTAGE - 1; ++k)
+        if (k < T) vr[k] = issue(k);
+    }
     // The first step's "previous sub-block" is the second half of stage NSTAGE-1's V tile
     // with P = 0: zero it so that 0 * V stays 0 (that stage is only filled after barrier 0).
     {
@@ -288,8 +318,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       unsigned char* zv = lds + V_BASE + (NSTAGE - 1) * TILE_B + HALF_B;
       *reinterpret_cast<u32x4*>(zv + 16 * threadIdx.x) = z;
     }
-    wait_tiles_outstanding(min(NSTAGE - 2, T - 1));
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero fill is done
+    if constexpr (!FP8) wait_tiles_outstanding(min(NSTAGE - 2, T - 1));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero fill (and fp8 tiles) are done
     barrier_nofence();
 
     // Pipeline registers, double-buffered so that consecutive steps swap roles instead of
@@ -319,101 +349,70 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     if (wave_active) {
 #pragma unroll
       for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
-      // first step's fragments: K of tile 0 half 1, V of the zeroed block
-      if (LBW_ATTN_XSTEP) {
-#pragma unroll
-        for (int i = 0; i < LDS_AHEAD; ++i)
-          load(std::integral_constant<int, HALF_B>{},
-               std::integral_constant<int, (NSTAGE - 1) * TILE_B + HALF_B>{}, i, i);
-      }
     }
 
-    // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow) into
-    // p_out, O += V^T p_in^T from LDS offset VO, s_out = K Q^T from LDS offset KO. With PRE
-    // the first LDS_AHEAD pairs' fragments were loaded by the previous step; with a nonzero
-    // next_c (NKO, NVO) this step loads the first pairs of the next step at its end (no
-    // barrier lies between them).
-    auto step = [&](auto koff_c, auto voff_c, auto pre_c, auto next_c, floatx16& s_in,
-                    floatx16& s_out, u32x4 (&p_in)[2], u32x4 (&p_out)[2], int kb, int vrow) {
-      constexpr int KO = decltype(koff_c)::value;
-      constexpr int VO = decltype(voff_c)::value;
-      constexpr bool PRE = decltype(pre_c)::value;
-      constexpr int NEXT = decltype(next_c)::value;  // NKO/HALF_B | NVO/HALF_B << 8, or -1
-      const auto ko_c = std::integral_constant<int, KO>{};
-      const auto vo_c = std::integral_constant<int, VO>{};
-      if constexpr (!PRE) {
+    // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow and,
+    // for fp8, block scales sk / sv) into p_out, O += V^T p_in^T from LDS offset VO,
+    // s_out = K Q^T from LDS offset KO.
+    auto step = [&](auto koff_c, auto voff_c, floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2],
+                    u32x4 (&p_out)[2], int kb, int vrow, float sk, float sv) {
 #pragma unroll
-        for (int i = 0; i < LDS_AHEAD; ++i) load(ko_c, vo_c, i, i);
-      }
+      for (int i = 0; i < LDS_AHEAD; ++i) load(koff_c, voff_c, i, i);
       if (pend) scale_acc(oacc, alpha_p);
       const int vlo = vrow & 0xffff, vhi = vrow >> 16;
       if (vlo > 32 * kb || vhi < 32 * kb + 32) mask_scores(s_in, kb, vlo, vhi, hl);
-      // softmax, part 1: running max and exponent reference (wave-uniform decision)
+      // softmax, part 1: running max and exponent reference (wave-uniform decision); fp8
+      // scores are q . k_code, the true score is that times the K block scale
       float mx = s_in[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
       mx = wave_max_xor32(mx);
+      if constexpr (FP8) mx *= sk;
       m_true = fmaxf(m_true, mx);
       const bool move = __any(m_true > m_used + tau_raw);
       const float m_new = move ? m_true : m_used;
       const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2((m_used - m_new) * c);
       m_used = m_new;
       const float mc = m_used == -INFINITY ? 0.0f : m_used * c;
+      // p = exp2(s_code sk c - m c), times sv for fp8 (V's scale, so that P^T V_code = P^T V)
+      const float cm = FP8 ? c * sk : c;
+      const float ca = FP8 ? __builtin_amdgcn_logf(sv) - mc : -mc;
       // MFMAs of the neighbouring sub-blocks
 #pragma unroll
       for (int r = 0; r < 16; ++r) s_out[r] = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        if (i + LDS_AHEAD < 8) load(ko_c, vo_c, i + LDS_AHEAD, (i + LDS_AHEAD) % (LDS_AHEAD + 1));
+        if (i + LDS_AHEAD < 8) load(koff_c, voff_c, i + LDS_AHEAD, (i + LDS_AHEAD) % (LDS_AHEAD + 1));
         s_out = mfma32x32x16(kf[i % (LDS_AHEAD + 1)], qf[i], s_out);
         oacc[i >> 1] = mfma32x32x16(vf[i % (LDS_AHEAD + 1)], p_in[i & 1], oacc[i >> 1]);
       }
-      if constexpr (NEXT >= 0) {
-#pragma unroll
-        for (int i = 0; i < LDS_AHEAD; ++i)
-          load(std::integral_constant<int, (NEXT & 0xff) * HALF_B>{},
-               std::integral_constant<int, (NEXT >> 8) * HALF_B>{}, i, i);
-      }
-      // softmax, part 2: P = exp2(s c - m c) packed to bf16 in the PV operand order; the row
-      // sum adds the bf16 values the PV MFMAs use (v_dot2 with (1, 1), two chains)
-      #if LBW_ATTN_DOT2_SUM
-      float ls0 = 0.0f, ls1 = 0.0f;
-#else
+      // softmax, part 2: P packed to bf16 in the PV operand order, fp32 row sum
       float ls = 0.0f;
-#endif
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], c, -mc));
-          const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], c, -mc));
+          const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], cm, ca));
+          const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], cm, ca));
           p_out[m][e] = pack_bf16x2(x0, x1);
-#if LBW_ATTN_DOT2_SUM
-          if (e & 1) ls1 = dot2_bf16_ones(p_out[m][e], ls1);
-          else ls0 = dot2_bf16_ones(p_out[m][e], ls0);
-#else
           ls += x0 + x1;
-#endif
         }
       }
-#if LBW_ATTN_DOT2_SUM
-      const float ls = ls0 + ls1;
-#endif
+      if constexpr (FP8) ls *= __builtin_amdgcn_rcpf(sv);
       lsum = __builtin_fmaf(lsum, alpha, ls);
       // keep the exponentials in this step's block (not sunk into the next one)
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
       // schedule: the first LDS_AHEAD pairs' fragments, then per MFMA pair: MFMA, 4 VALU,
       // MFMA, 4 VALU, the 3 LDS reads of the pair LDS_AHEAD ahead
-      if constexpr (!PRE) __builtin_amdgcn_sched_group_barrier(0x100, 3 * LDS_AHEAD, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 3 * LDS_AHEAD, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, LBW_ATTN_VALU_A, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, LBW_ATTN_VALU_B, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
         if (i + LDS_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // 3 LDS reads
       }
-      if constexpr (NEXT >= 0) __builtin_amdgcn_sched_group_barrier(0x100, 3 * LDS_AHEAD, 0);
       pend = move;
       alpha_p = alpha;
     };
@@ -428,22 +427,36 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       constexpr int SP = (ST + NSTAGE - 1) % NSTAGE;  // stage of tile u-1
       constexpr int SN = (ST + 1) % NSTAGE;           // stage of tile u+1
       const int vrow = vr[0];
+      const float sk = skr[0], sv = svr[0];
       if (wave_active)
         step(std::integral_constant<int, ST * TILE_B + HALF_B>{},
-             std::integral_constant<int, SP * TILE_B + HALF_B>{},
-             std::integral_constant<bool, LBW_ATTN_XSTEP != 0>{},
-             std::integral_constant<int, -1>{}, sA, sB, pA, pB, 0, vrow);
-      if (u + 1 < T) wait_tiles_outstanding(min(NSTAGE - 3, T - 2 - u));
+             std::integral_constant<int, SP * TILE_B + HALF_B>{}, sA, sB, pA, pB, 0, vrow, sk, sv);
+      if constexpr (FP8) {
+        // tile u+1 (loaded one tile ago) into its stage, the one tile u-2 left
+        if (u >= 1 && u + 1 < T) write8(SN);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the LDS writes are done
+      } else {
+        if (u + 1 < T) wait_tiles_outstanding(min(NSTAGE - 3, T - 2 - u));
+      }
       barrier_nofence();
-      if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = issue(SP);
-      // the next step (tile u+1 half 0 softmax): K of tile u+1 half 1, V of tile u half 1
-      constexpr int NEXT = LBW_ATTN_XSTEP ? (2 * SN + 1) | ((2 * ST + 1) << 8) : -1;
+      if constexpr (FP8) {
+        if (u + 2 < T) {
+          vr[2] = issue8();
+          skr[2] = sk_n;
+          svr[2] = sv_n;
+        }
+      } else {
+        if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = issue(SP);
+      }
       if (wave_active)
         step(std::integral_constant<int, SN * TILE_B>{},
-             std::integral_constant<int, ST * TILE_B>{}, std::false_type{},
-             std::integral_constant<int, NEXT>{}, sB, sA, pB, pA, 1, vrow);
+             std::integral_constant<int, ST * TILE_B>{}, sB, sA, pB, pA, 1, vrow, sk, sv);
 #pragma unroll
-      for (int k = 0; k < NSTAGE - 1; ++k) vr[k] = vr[k + 1];
+      for (int k = 0; k < NSTAGE - 1; ++k) {
+        vr[k] = vr[k + 1];
+        skr[k] = skr[k + 1];
+        svr[k] = svr[k + 1];
+      }
     };
 
 #pragma unroll 1
@@ -451,8 +464,6 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       tile(std::integral_constant<int, 0>{}, u);
       if (u + 1 < T) tile(std::integral_constant<int, 1>{}, u + 1);
       if (u + 2 < T) tile(std::integral_constant<int, 2>{}, u + 2);
-      if constexpr (NSTAGE == 4)
-        if (u + 3 < T) tile(std::integral_constant<int, 3 % NSTAGE>{}, u + 3);
     }
 
     // drain: O += V^T P^T of the last sub-block (tile T-1 half 1, P in pA)
@@ -522,13 +533,22 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel,
+template <bool FP8>
+static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t nwg = (uint32_t)a.n_qtiles * a.splits * a.H * a.B;
-  hipLaunchKernelGGL(attn_fwd_bf16_kernel, dim3(nwg), dim3(NWAVE * 64), LDS_B, stream, a);
+  hipLaunchKernelGGL(attn_fwd_bf16_kernel<FP8>, dim3(nwg), dim3(NWAVE * 64), LDS_B, stream, a);
   return hipGetLastError();
+}
+
+hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
+  return launch<false>(a, stream);
+}
+
+hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {
+  return launch<true>(a, stream);
 }
 
 }  // namespace lbw

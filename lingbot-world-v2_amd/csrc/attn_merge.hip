@@ -1,0 +1,60 @@
+// Log-sum-exp merge of split-KV attention partials (gfx950), the cte_merge contract of
+// wan/modules/attention.py:963-990: given per split s the unnormalised O_s (relative to the
+// split's row max), the row max m_s (scaled scores) and the row sum l_s,
+//   out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s,  M = max_s m_s,
+// written as bf16; a row whose every split is empty (all m_s = -inf) yields 0.
+//
+// HBM-bound: per (b, h, q) row it reads n * (D + 2) fp32 values and writes D bf16 values.
+// One thread per (row, 4 consecutive d), so every load and store is a 16 / 8-byte vector.
+
+#include "attn_tiles.h"
+
+namespace lbw {
+
+__global__ void __launch_bounds__(256)
+attn_merge_kernel(const MergeKernelArgs a) {
+  const int64_t total = (int64_t)a.B * a.H * a.Lq * (a.D / 4);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int dq = (int)(i % (a.D / 4));
+    const int64_t row = i / (a.D / 4);  // (b*H + h)*Lq + q
+    const int q = (int)(row % a.Lq);
+    const int64_t bh = row / a.Lq;
+    const int h = (int)(bh % a.H);
+    const int b = (int)(bh / a.H);
+    float M = -INFINITY;
+    for (int s = 0; s < a.n; ++s) M = fmaxf(M, a.m[s][row]);
+    float den = 0.0f;
+    floatx4 num = {0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
+      for (int s = 0; s < a.n; ++s) {
+        const float ms = a.m[s][row];
+        const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);
+        den += w * a.l[s][row];
+        const floatx4 o = *reinterpret_cast<const floatx4*>(a.o[s] + row * a.D + 4 * dq);
+        num += w * o;
+      }
+    }
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)q + a.osh * h + 4 * dq;
+    u32x2 w;
+    w[0] = pack_bf16x2(num[0] * inv, num[1] * inv);
+    w[1] = pack_bf16x2(num[2] * inv, num[3] * inv);
+    *reinterpret_cast<u32x2*>(op) = w;
+  }
+}
+
+// Work-decomposition constants of the attention kernels, for the host-side planning.
+int attn_block_m() { return 256; }
+int attn_block_n() { return BN; }
+
+hipError_t launch_attn_merge(const MergeKernelArgs& a, hipStream_t stream) {
+  const int64_t total = (int64_t)a.B * a.H * a.Lq * (a.D / 4);
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace lbw
