@@ -160,9 +160,12 @@ def other_configs(dev):
     q = rnd(1, 4680, 40, D)
     kx, vx = rnd(1, 512, 40, D), rnd(1, 512, 40, D)
     kl = torch.tensor([300], dtype=torch.int32, device=dev)
-    for name, lens, nk in (("wan14b_480p_cross_512ctx_300valid", kl, 300),
-                           ("wan14b_480p_cross_512ctx_unmasked", None, 512)):
-        ms = _time_ms(lambda: cross_attention(q, kx, vx, k_lens=lens), iters=20)
+    kx[:, 300:] = kx[:, 511:]   # identical padding rows, as the projected zero padding gives
+    vx[:, 300:] = vx[:, 511:]
+    for name, lens, nk, nd in (("wan14b_480p_cross_512ctx_300valid", kl, 300, None),
+                               ("wan14b_480p_cross_512ctx_unmasked", None, 512, None),
+                               ("wan14b_480p_cross_512ctx_unmasked_dedup", None, 512, 300)):
+        ms = _time_ms(lambda: cross_attention(q, kx, vx, k_lens=lens, n_distinct=nd), iters=20)
         fl = 4.0 * 4680 * nk * D * 40
         by = 2.0 * (2 * 4680 + 2 * nk) * 40 * D
         out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),

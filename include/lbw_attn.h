@@ -16,6 +16,10 @@
  *                          kernels/attention_cte_lb.py:270     attention_cte
  *   lbw_cross_attention_fwd wan/modules/attention.py:280-311   _nki_cross_attention
  *                          kernels/cross_attention.py:17       wan_cross_attn
+ *   lbw_cross_attention_dedup_fwd
+ *                          wan/modules/attention.py:493-554    cross_dedup_bias +
+ *                                                              cross_attention_dedup
+ *                          kernels/cross_dedup.py              cross_dedup_kernel
  *   lbw_attn_merge         wan/modules/attention.py:963-990    cte_merge
  *   lbw_qk_norm_rope       kernels/qk_post.py:404-413          qk_ss + qk_norm_rope
  *                          (caller wan/modules/model_fast.py:2596-2681 _qkv_post)
@@ -89,6 +93,13 @@ int lbw_attention_fwd(const lbw_attn_params* p, void* workspace, size_t workspac
 /* Cross-attention to a short context (one segment of <= 4096 keys, typically 512), with the
  * optional per-batch valid length p->k_lens. Single pass, no workspace. */
 int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream);
+
+/* Exact deduplicated cross-attention (no mask): keys n_distinct .. len-1 of the one segment
+ * must be identical rows (the context's zero padding after the projections); the result equals
+ * attention over all len keys, computed over the distinct keys plus the r identical ones up to
+ * the end of their 64-key tile, each of those with its score raised by ln((len - n_distinct) /
+ * r). p->k_lens must be NULL and no window set. */
+int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, void* stream);
 
 /* fp8-e4m3 KV cache: K/V segments hold e4m3fn codes with per-(batch, head, 64-token block)
  * fp32 scales (lbw_kv_quant_fp8's layout); Q stays bf16. */

@@ -39,6 +39,8 @@ struct AttnKernelArgs {
   float* part_o;
   float* part_m;
   float* part_l;
+  int64_t mult_key;   // first of the keys that each stand for several identical keys, or -1
+  float mult_raw;     // ln(multiplicity) / scale: added to those keys' raw scores
 };
 
 struct MergeKernelArgs {

@@ -100,14 +100,30 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
-// Scores of keys outside the tile's valid rows [tvlo, tvhi) -> -inf (S^T register layout).
-__device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int tvhi, int hl) {
+// Scores of keys outside the tile's valid rows [tvlo, tvhi) -> -inf (S^T register layout);
+// rows from mrow on get `add` (the log-multiplicity of deduplicated keys).
+__device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int tvhi, int hl,
+                                            int mrow, float add) {
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int key = 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3);
+    if (key >= mrow) sc[r] += add;
     if (key < tvlo || key >= tvhi) sc[r] = -INFINITY;
   }
+}
+
+// Packed per-tile row info: valid rows [vlo, vhi) and the first row carrying the
+// multiplicity bias (every key from a.mult_key on does; 255: none), from the cursor's tile.
+__device__ __forceinline__ int tile_rows(const AttnKernelArgs& a, const TileCursor& cs) {
+  int tvlo, tvhi;
+  cursor_rows(cs, tvlo, tvhi);
+  int mrow = 255;
+  if (a.mult_key >= 0) {
+    const int64_t r = a.mult_key - (a.seg[cs.seg].start + cs.lt * BN);
+    if (r < tvhi) mrow = r > tvlo ? (int)r : tvlo;
+  }
+  return tvlo | (tvhi << 8) | (mrow << 16);
 }
 
 __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
@@ -211,8 +227,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   const float c = a.scale_log2;
   const float tau_raw = TAU / c;
 
-  // DMA of the cursor's tile into a stage (2*NDMA x 16 B per lane); returns the tile's valid
-  // rows packed as vlo | vhi << 16. Full tiles use the per-segment lane offsets; in a partial
+  // DMA of the cursor's tile into a stage (2*NDMA x 16 B per lane); returns the tile's row
+  // info (tile_rows). Full tiles use the per-segment lane offsets; in a partial
   // tile, rows outside the valid range fetch a valid row instead: their scores are masked to
   // -inf and their probabilities are exactly 0, so the duplicate never contributes.
   TileCursor cs;
@@ -226,8 +242,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   };
   const uint32_t lds_wave = lds_addr(lds) + 1024 * NDMA * wave;  // this wave's 1 KB blocks
   auto issue = [&](int stage) -> int {
-    int tvlo, tvhi;
-    cursor_rows(cs, tvlo, tvhi);
+    const int rows = tile_rows(a, cs);
+    const int tvlo = rows & 0xff, tvhi = (rows >> 8) & 0xff;
     const int64_t row0 = cs.lt * BN;
     const unsigned char* kb = cs.kbase + row0 * cs.ks;
     const unsigned char* vb = cs.vbase + row0 * cs.vs;
@@ -250,7 +266,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
     }
     if (cursor_next<ESZ>(a, lo, hi, b, h, cs) && cs.seg < a.nseg) seg_offsets();
-    return tvlo | (tvhi << 16);
+    return rows;
   };
 
   // fp8: thread t stages row t/8, 16-byte code chunk t%8 (bf16 logical chunks 2(t%8), +1) of
@@ -259,8 +275,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   u32x4 k8 = {0u, 0u, 0u, 0u}, v8 = {0u, 0u, 0u, 0u};
   float sk_n = 1.0f, sv_n = 1.0f;
   auto issue8 = [&]() -> int {
-    int tvlo, tvhi;
-    cursor_rows(cs, tvlo, tvhi);
+    const int rows = tile_rows(a, cs);
+    const int tvlo = rows & 0xff, tvhi = (rows >> 8) & 0xff;
     const int64_t row0 = cs.lt * BN;
     int r = row8;
     r = r < tvlo ? tvlo : (r > tvhi - 1 ? tvhi - 1 : r);
@@ -269,7 +285,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     sk_n = cs.ksc[cs.lt];
     sv_n = cs.vsc[cs.lt];
     cursor_next<1>(a, lo, hi, b, h, cs);
-    return tvlo | (tvhi << 16);
+    return rows;
   };
   auto write8 = [&](int stage) {
     auto cvt = [](const u32x4& x, int half) {
@@ -294,7 +310,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     int vr[NSTAGE];  // valid rows of tiles u .. u+NSTAGE-1 (u = the tile being softmaxed)
     float skr[NSTAGE], svr[NSTAGE];  // fp8 block scales of the same tiles
 #pragma unroll
-    for (int k = 0; k < NSTAGE; ++k) { vr[k] = BN << 16; skr[k] = 1.0f; svr[k] = 1.0f; }
+    for (int k = 0; k < NSTAGE; ++k) { vr[k] = (BN << 8) | (255 << 16); skr[k] = 1.0f; svr[k] = 1.0f; }
     cursor_init<ESZ>(a, lo, hi, t0, b, h, cs);
     if constexpr (FP8) {
 #pragma unroll
@@ -359,8 +375,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 #pragma unroll
       for (int i = 0; i < LDS_AHEAD; ++i) load(koff_c, voff_c, i, i);
       if (pend) scale_acc(oacc, alpha_p);
-      const int vlo = vrow & 0xffff, vhi = vrow >> 16;
-      if (vlo > 32 * kb || vhi < 32 * kb + 32) mask_scores(s_in, kb, vlo, vhi, hl);
+      const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
+      if (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32)
+        mask_scores(s_in, kb, vlo, vhi, hl, mrow, a.mult_raw);
       // softmax, part 1: running max and exponent reference (wave-uniform decision); fp8
       // scores are q . k_code, the true score is that times the K block scale
       float mx = s_in[0];

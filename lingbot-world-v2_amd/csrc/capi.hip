@@ -147,6 +147,7 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
 
   AttnKernelArgs& a = plan->a;
   memset(&a, 0, sizeof(a));
+  a.mult_key = -1;
   a.q = static_cast<const uint16_t*>(p->q);
   a.qsb = p->q_stride_b; a.qsl = p->q_stride_l; a.qsh = p->q_stride_h;
   a.out = static_cast<uint16_t*>(p->out);
@@ -213,12 +214,17 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   return LBW_OK;
 }
 
-int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes, void* stream) {
+int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes, void* stream,
+                  int64_t mult_key = -1, double mult = 1.0) {
   Plan plan;
   int rc = make_plan(p, fp8, &plan);
   if (rc != LBW_OK) return rc;
   if (p->lq == 0) return LBW_OK;
   AttnKernelArgs& a = plan.a;
+  if (mult_key >= 0) {
+    a.mult_key = mult_key;
+    a.mult_raw = (float)(log(mult) / (double)a.scale);
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (plan.splits > 1) {
     if (ws == nullptr || ws_bytes < plan.ws_bytes || !aligned16(ws))
@@ -279,6 +285,33 @@ int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream) {
   lbw_attn_params q = *p;
   q.num_splits = 1;
   return run_attention(&q, false, nullptr, 0, stream);
+}
+
+int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, void* stream) {
+  if (p == nullptr) return fail(LBW_ERR_INVALID, "params is NULL");
+  if (p->n_segments != 1) return fail(LBW_ERR_INVALID, "cross-attention takes one KV segment");
+  const int64_t L = p->seg[0].len;
+  if (L > 4096)
+    return fail(LBW_ERR_INVALID, "cross-attention context of %lld keys exceeds 4096", (long long)L);
+  if (n_distinct < 0 || n_distinct > L)
+    return fail(LBW_ERR_INVALID, "n_distinct %lld not in [0, %lld]", (long long)n_distinct,
+                (long long)L);
+  if (p->k_lens != nullptr || p->kv_lo != 0 || p->kv_hi >= 0)
+    return fail(LBW_ERR_INVALID, "dedup attends the whole context: no k_lens or window");
+  if (p->num_splits > 1) return fail(LBW_ERR_INVALID, "cross-attention is single pass");
+  lbw_attn_params q = *p;
+  q.num_splits = 1;
+  if (n_distinct == L) return run_attention(&q, false, nullptr, 0, stream);
+  // The distinct keys plus the r identical ones up to the end of their 64-key tile (free: the
+  // tile is read anyway), each of those weighted m / r (m = L - n_distinct identical rows in
+  // all): cross_dedup_bias's log(m / r) form. Spreading the weight over r bf16 probabilities
+  // keeps the rounding error of that dominant term close to the undeduplicated call's.
+  const int64_t bn = attn_block_n();
+  const int64_t end = std::min<int64_t>(L, (n_distinct / bn + 1) * bn);
+  q.kv_lo = 0;
+  q.kv_hi = end;
+  return run_attention(&q, false, nullptr, 0, stream, n_distinct,
+                       (double)(L - n_distinct) / (double)(end - n_distinct));
 }
 
 int lbw_attention_fwd_fp8kv(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,

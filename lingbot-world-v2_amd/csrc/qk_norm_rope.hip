@@ -22,7 +22,6 @@
 namespace lbw {
 
 constexpr int QK_WAVES = 4;
-constexpr int QK_MAX_NCH = 16;             // chunks of 8 per lane: C <= 16 * 64 * 8 = 8192
 constexpr int QK_MAX_TABLE = 16384;        // floats of per-axis tables held in LDS (64 KB)
 
 int qk_norm_rope_max_table_floats() { return QK_MAX_TABLE; }

@@ -92,13 +92,15 @@ def _params(q, out, segments, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, p
 def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi=None,
                        k_lens: torch.Tensor | None = None, softmax_scale=None,
                        num_splits: int = 0, out: torch.Tensor | None = None,
-                       cross: bool = False) -> torch.Tensor:
+                       cross: bool = False, n_distinct: int | None = None) -> torch.Tensor:
     """softmax(scale Q K^T) V over the windowed concatenation of KV ``segments``.
 
     q ``[B, Lq, N, 128]``; each segment is ``(k, v)`` with k/v ``[B, L_i, N, 128]`` (strided
     views are fine as long as the head dim is contiguous); the window ``[kv_lo, kv_hi)``
     indexes the concatenation. ``k_lens`` (int32 ``[B]`` on the device) limits each batch's
-    keys. Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given)."""
+    keys. With ``cross``, a single short segment; ``n_distinct`` (cross only) declares keys
+    ``n_distinct..`` identical rows, attended as one key of that multiplicity (exact).
+    Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given)."""
     lib = _lib.load()
     device = q.device
     _check_4d("q", q, device)
@@ -115,7 +117,10 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     p = _params(q, out, segs, kv_lo, kv_hi, k_lens, softmax_scale, 1 if cross else num_splits)
     stream = _lib.stream_ptr(device)
     with torch.cuda.device(device):
-        if cross:
+        if cross and n_distinct is not None:
+            _lib.check(lib.lbw_cross_attention_dedup_fwd(ctypes_ref(p), int(n_distinct), stream),
+                       "lbw_cross_attention_dedup_fwd")
+        elif cross:
             _lib.check(lib.lbw_cross_attention_fwd(ctypes_ref(p), stream), "lbw_cross_attention_fwd")
         else:
             ws_bytes = lib.lbw_attention_workspace_size(ctypes_ref(p))
@@ -201,12 +206,33 @@ def exact_attention_chunks(q, k_chunks, v_chunks, dtype=torch.bfloat16):
     return out if dtype == torch.bfloat16 else out.to(dtype)
 
 
-def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16):
+def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16, n_distinct=None):
     """Cross-attention to a short context (kernels/cross_attention.py:17 semantics), with the
     optional per-batch valid length ``k_lens`` masked (the reference attends all rows;
-    ``k_lens=None`` reproduces that)."""
-    out = attention_segments(q, [(k, v)], k_lens=k_lens, cross=True)
+    ``k_lens=None`` reproduces that). ``n_distinct`` selects the exact deduplicated form of
+    attention.py:493-554: rows ``n_distinct..`` of k/v are identical (the context's padding)
+    and are attended as one key weighted by their count (see ``padding_start``)."""
+    if n_distinct is not None and k_lens is not None:
+        raise ValueError("dedup reproduces the unmasked attention: pass k_lens or n_distinct")
+    out = attention_segments(q, [(k, v)], k_lens=k_lens, cross=True, n_distinct=n_distinct)
     return out if dtype == torch.bfloat16 else out.to(dtype)
+
+
+def padding_start(k: torch.Tensor, v: torch.Tensor) -> int:
+    """Index of the first of the trailing rows of a cross K/V cache ``[1, L, N, D]`` that equal
+    its last row in both K and V (the projected zero padding of the context;
+    cross_dedup_bias, attention.py:493-503, counts the same rows); L when there is none.
+    One device sync: call it once per context (the cross cache is filled once per
+    generation)."""
+    if k.shape[0] != 1 or v.shape[0] != 1:
+        raise ValueError("padding_start expects batch 1")
+    same = ((k[0] == k[0, -1:]).flatten(1).all(dim=1) & (v[0] == v[0, -1:]).flatten(1).all(dim=1))
+    L = same.shape[0]
+    # length of the trailing run of identical rows
+    idx = torch.arange(L, device=k.device)
+    last_diff = torch.where(~same, idx, torch.full_like(idx, -1)).max()
+    start = int(last_diff.item()) + 1
+    return start if start < L else L
 
 
 def attention_partial(q, segments, *, kv_lo=None, kv_hi=None, softmax_scale=None):

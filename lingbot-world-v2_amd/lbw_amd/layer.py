@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from .attention import attention_segments, cross_attention
+from .attention import attention_segments, cross_attention, padding_start
 from .chunked_kv_cache import FlatKVCache, chunk_routing, ordered_chunks
 from .qk_post import qk_norm_rope_
 from .rope import RopeTables, causal_rope_tables, wan_rope_freqs
@@ -103,14 +103,17 @@ class WanSelfAttention:
 class WanCrossAttention:
     """Cross-attention of one Wan block to the text context, with the per-generation cache."""
 
-    def __init__(self, wq, bq, wk, bk, wv, bv, wo, bo, gq, gk, heads: int, eps: float = 1e-6):
+    def __init__(self, wq, bq, wk, bk, wv, bv, wo, bo, gq, gk, heads: int, eps: float = 1e-6,
+                 dedup: bool = False):
         self.C = wq.shape[0]
         self.heads = heads
         self.head_dim = self.C // heads
         self.eps = eps
         self.wq, self.bq, self.wk, self.bk, self.wv, self.bv = wq, bq, wk, bk, wv, bv
         self.wo, self.bo, self.gq, self.gk = wo, bo, gq, gk
+        self.dedup = dedup      # attention.py:516-554: identical padding rows as one weighted key
         self.cache = None
+        self.n_distinct = None
 
     def _norm(self, x_raw, bias, gamma):
         """RMSNorm of projected rows [L, C] (no rotation) through the fused kernel."""
@@ -129,6 +132,7 @@ class WanCrossAttention:
         Lc = ctx.shape[0]
         self.cache = (k.view(1, Lc, self.heads, self.head_dim),
                       v.contiguous().view(1, Lc, self.heads, self.head_dim))
+        self.n_distinct = padding_start(*self.cache) if self.dedup else None
 
     def forward(self, x, context=None, k_lens=None):
         """x [1, L, C] -> [1, L, C]; ``k_lens`` (int32 [1] on the device) masks the context's
@@ -138,6 +142,7 @@ class WanCrossAttention:
         L = x.shape[1]
         q = self._norm(F.linear(x[0], self.wq).contiguous(), self.bq, self.gq)
         k, v = self.cache
-        o = cross_attention(q.view(1, L, self.heads, self.head_dim), k, v, k_lens=k_lens)
+        o = cross_attention(q.view(1, L, self.heads, self.head_dim), k, v, k_lens=k_lens,
+                            n_distinct=self.n_distinct if k_lens is None else None)
         return F.linear(o.view(1, L, self.C), self.wo, self.bo)
 

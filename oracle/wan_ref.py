@@ -17,7 +17,7 @@ __all__ = [
     "attention_brute_f64", "merge_partials", "window_mask", "num_chunks", "chunk_routing",
     "ordered_chunks", "flat_cache_write_plan", "fp8_e4m3_encode", "fp8_e4m3_decode",
     "quantize_kv_fp8", "dequantize_kv_fp8", "self_attention_layer_ref", "cross_kv_ref",
-    "attn_flops", "cosine",
+    "attn_flops", "cosine", "cross_dedup_bias", "attention_key_bias_ref",
 ]
 
 # wan/modules/model.py:44 -- rows of the RoPE frequency tables (frame axis bound).
@@ -427,6 +427,28 @@ def self_attention_layer_ref(x, x_cache, wq, bq, wk, bk, wv, bv, wo, bo, gq, gk,
     vv = torch.cat([vc, v], 0)[None]
     o = attention_ref(q[None], kk, vv)
     return o.reshape(1, -1, C) @ wo.float().T + bo.float()
+
+
+def cross_dedup_bias(k, v, kc: int):
+    """attention.py:493-503 ``cross_dedup_bias``: over the first kc rows of K / V ``[L, n, d]``,
+    log(m / r) on the r rows of the slice that equal the last row in both K and V (m such rows
+    in all), 0 elsewhere (fp32 ``[kc]``)."""
+    same = (k == k[-1:]).flatten(1).all(dim=1) & (v == v[-1:]).flatten(1).all(dim=1)
+    s = same[:kc]
+    m, r = same.sum().float(), s.sum().float()
+    return torch.where(s, torch.log(m / r), torch.zeros((), dtype=torch.float32))
+
+
+def attention_key_bias_ref(q, k, v, bias, softmax_scale=None):
+    """softmax(scale q k^T + bias) v with a per-key additive bias (natural-log units), fp32,
+    q ``[B, Lq, H, D]``, k/v ``[B, Lk, H, D]``, bias ``[Lk]`` (attention.py:546-554)."""
+    D = q.shape[-1]
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(D)
+    qh = q.float().permute(0, 2, 1, 3)
+    kh = k.float().permute(0, 2, 3, 1)
+    vh = v.float().permute(0, 2, 1, 3)
+    p = torch.softmax(torch.matmul(qh, kh) * scale + bias.float(), dim=-1)
+    return torch.matmul(p, vh).permute(0, 2, 1, 3)
 
 
 def cross_kv_ref(context, wk, bk, wv, bv, gk, heads: int, eps: float = 1e-6):

@@ -183,3 +183,35 @@ def test_full_size_wan13b_480p_chunk(lib):
 def test_full_size_wan14b_720p_chunk(lib):
     """14B 720p: 1-frame chunk (3600 q) over 12 cached frames + chunk (46800 keys), 40 heads."""
     _full_size_subset(40, 3600, 43200, 3600, heads=[0, 19, 39], rows=256, seed=2)
+
+
+def test_cross_attention_dedup_matches_full_context():
+    """Exact dedup (attention.py:493-554): a 512-row context whose rows 300.. are identical
+    (the projected zero padding); the deduplicated call equals unmasked attention over all
+    512 rows (oracle) and the plain unmasked kernel call."""
+    from lbw_amd import cross_attention, padding_start
+    g = torch.Generator().manual_seed(41)
+    H, Lq, L, nv = 4, 333, 512, 300
+    q = torch.randn(1, Lq, H, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, L, H, 128, generator=g)
+    # V at half scale: the padding row carries 212/512 of the keys, so outputs follow it
+    # closely; this keeps |o| < 2, where one bf16 output rounding stays within the 1e-2 bound
+    v = 0.5 * torch.randn(1, L, H, 128, generator=g)
+    k[:, nv:] = torch.randn(1, 1, H, 128, generator=g)
+    v[:, nv:] = 0.5 * torch.randn(1, 1, H, 128, generator=g)
+    k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    nd = padding_start(kd, vd)
+    assert nd == nv
+    out = cross_attention(q.to(DEV), kd, vd, n_distinct=nd)
+    ref = O.attention_ref(q, k, v)
+    assert_parity(out, ref, "dedup")
+    plain = cross_attention(q.to(DEV), kd, vd)
+    assert float((out.float() - plain.float()).abs().max()) <= 1e-2
+    # no padding at all: n_distinct = L - 1 (the last row counts once)
+    k2 = torch.randn(1, 96, H, 128, generator=g).to(torch.bfloat16)
+    v2 = torch.randn(1, 96, H, 128, generator=g).to(torch.bfloat16)
+    nd2 = padding_start(k2.to(DEV), v2.to(DEV))
+    assert nd2 == 95
+    out2 = cross_attention(q.to(DEV), k2.to(DEV), v2.to(DEV), n_distinct=nd2)
+    assert_parity(out2, O.attention_ref(q, k2, v2), "dedup, no padding")

@@ -106,3 +106,30 @@ def test_wan14b_cross_attention_layer(lib):
     o = O.attention_ref(q.view(1, -1, H, 128), kk, vv, k_lens=[300])
     ref = o.reshape(1, -1, C) @ f["wo"].T + f["bo"]
     _check(out[:, rows], ref, "cross")
+
+
+def test_wan14b_cross_attention_layer_dedup(lib):
+    """The same 14B cross-attention with the reference's unmasked semantics (all 512 context
+    rows attended) computed by the exact dedup: the 212 zero-padding rows project to identical
+    K/V rows and are attended as one key of multiplicity 212."""
+    from lbw_amd import WanCrossAttention
+    g = torch.Generator().manual_seed(4)
+    C, H, Lq = 5120, 40, 1560
+    ctx_raw = torch.randn(1, 512, 4096, generator=g)
+    ctx_raw[:, 300:] = 0
+    w_text = _w(g, C, 4096)
+    ctx = (ctx_raw.to(torch.bfloat16).float() @ w_text.float().T).to(torch.bfloat16)
+    x = torch.randn(1, Lq, C, generator=g).to(torch.bfloat16)
+    ws = _weights(C, g, 0.02, 0.05)
+    d = {k: v.to(DEV) for k, v in ws.items()}
+    layer = WanCrossAttention(d["wq"], d["bq"], d["wk"], d["bk"], d["wv"], d["bv"], d["wo"],
+                              d["bo"], d["gq"], d["gk"], heads=H, dedup=True)
+    out = layer.forward(x.to(DEV), ctx.to(DEV))
+    assert layer.n_distinct == 300
+    rows = torch.randperm(Lq, generator=g)[:192].sort().values
+    f = {k: v.float() for k, v in ws.items()}
+    q = O.rms_norm_module(x[:, rows].float() @ f["wq"].T + f["bq"], f["gq"])
+    kk, vv = O.cross_kv_ref(ctx.float(), f["wk"], f["bk"], f["wv"], f["bv"], f["gk"], H)
+    o = O.attention_ref(q.view(1, -1, H, 128), kk, vv)
+    ref = o.reshape(1, -1, C) @ f["wo"].T + f["bo"]
+    _check(out[:, rows], ref, "cross dedup")

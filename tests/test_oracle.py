@@ -356,3 +356,25 @@ def test_cross_kv_ref_closed_forms():
     # per-row RMS of K / gamma is 1 (the norm's defining property)
     kk = (k1[0, :7].reshape(7, C) / gk)
     assert torch.allclose(kk.pow(2).mean(-1), torch.ones(7), atol=1e-4)
+
+
+def test_cross_dedup_forms_equal_full_attention():
+    """attention.py:516-523: identical padding rows can share one softmax term weighted by their
+    count. Full attention over all L rows == the reference's kc-row slice with the
+    cross_dedup_bias == the minimal form (distinct rows + one padding row, bias log(m))."""
+    g = torch.Generator().manual_seed(31)
+    L, n_valid, H, D = 64, 23, 2, 16
+    k = torch.randn(1, L, H, D, generator=g)
+    v = torch.randn(1, L, H, D, generator=g)
+    k[:, n_valid:] = torch.randn(1, 1, H, D, generator=g)    # padding rows: one repeated row
+    v[:, n_valid:] = torch.randn(1, 1, H, D, generator=g)
+    q = torch.randn(1, 9, H, D, generator=g)
+    full = O.attention_ref(q, k, v)
+    kc = 32
+    bias = O.cross_dedup_bias(k[0], v[0], kc)
+    assert int((bias != 0).sum()) == kc - n_valid
+    ref_form = O.attention_key_bias_ref(q, k[:, :kc], v[:, :kc], bias)
+    minimal_bias = torch.zeros(n_valid + 1)
+    minimal_bias[-1] = math.log(L - n_valid)
+    minimal = O.attention_key_bias_ref(q, k[:, :n_valid + 1], v[:, :n_valid + 1], minimal_bias)
+    assert torch.allclose(ref_form, full, atol=1e-5) and torch.allclose(minimal, full, atol=1e-5)
