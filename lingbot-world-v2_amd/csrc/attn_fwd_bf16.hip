@@ -52,7 +52,8 @@ constexpr int NSTAGE = 3;               // tiles resident or in flight
 constexpr int V_BASE = 65536;           // V tiles start here; K tiles at NSTAGE * 16 KB below
 constexpr int LDS_B = V_BASE + NSTAGE * TILE_B;
 constexpr int NDMA = TILE_B / (NWAVE * 64 * 16);  // 16-byte DMA blocks per lane per K/V tile
-constexpr int LDS_AHEAD = 2;                      // MFMA pairs of LDS fragments in flight
+// MFMA pairs ahead that a step's K (QK chain) and V (PV) fragments are read from LDS
+constexpr int K_AHEAD = 2, V_AHEAD = 2;
 static_assert(NSTAGE * TILE_B <= V_BASE, "K tiles must fit below the V tiles");
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
@@ -350,22 +351,19 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     bool pend = false;
     float alpha_p = 1.0f;
 
-    // LDS fragments of the MFMA pairs in flight (pair i of a step uses buffer i % (LDS_AHEAD+1))
-    u32x4 kf[LDS_AHEAD + 1], vf[LDS_AHEAD + 1];
-    auto load = [&](auto ko_c, auto vo_c, int i, int buf) {
+    // LDS fragments in flight: K of pair i in kf[i % (K_AHEAD + 1)], V in vf[i % (V_AHEAD + 1)]
+    u32x4 kf[K_AHEAD + 1], vf[V_AHEAD + 1];
+    auto load_k = [&](auto ko_c, int i) {
       constexpr int KO = decltype(ko_c)::value;
+      kf[i % (K_AHEAD + 1)] = lds_read_b128(koff[i] + KO);
+    };
+    auto load_v = [&](auto vo_c, int i) {
       constexpr int VO = decltype(vo_c)::value;
-      kf[buf] = lds_read_b128(koff[i] + KO);
       const int db = i >> 1, m = i & 1;
       const u32x2 v0 = lds_read_tr16(voff[db][0] + VO + 16 * m * ROWB);
       const u32x2 v1 = lds_read_tr16(voff[db][1] + VO + 16 * m * ROWB);
-      vf[buf] = u32x4{v0[0], v0[1], v1[0], v1[1]};
+      vf[i % (V_AHEAD + 1)] = u32x4{v0[0], v0[1], v1[0], v1[1]};
     };
-
-    if (wave_active) {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
-    }
 
     // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow and,
     // for fp8, block scales sk / sv) into p_out, O += V^T p_in^T from LDS offset VO,
@@ -373,7 +371,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     auto step = [&](auto koff_c, auto voff_c, floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2],
                     u32x4 (&p_out)[2], int kb, int vrow, float sk, float sv) {
 #pragma unroll
-      for (int i = 0; i < LDS_AHEAD; ++i) load(koff_c, voff_c, i, i);
+      for (int i = 0; i < K_AHEAD; ++i) load_k(koff_c, i);
+#pragma unroll
+      for (int i = 0; i < V_AHEAD; ++i) load_v(voff_c, i);
       if (pend) scale_acc(oacc, alpha_p);
       const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
       if (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32)
@@ -399,9 +399,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       for (int r = 0; r < 16; ++r) s_out[r] = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        if (i + LDS_AHEAD < 8) load(koff_c, voff_c, i + LDS_AHEAD, (i + LDS_AHEAD) % (LDS_AHEAD + 1));
-        s_out = mfma32x32x16(kf[i % (LDS_AHEAD + 1)], qf[i], s_out);
-        oacc[i >> 1] = mfma32x32x16(vf[i % (LDS_AHEAD + 1)], p_in[i & 1], oacc[i >> 1]);
+        if (i + K_AHEAD < 8) load_k(koff_c, i + K_AHEAD);
+        if (i + V_AHEAD < 8) load_v(voff_c, i + V_AHEAD);
+        s_out = mfma32x32x16(kf[i % (K_AHEAD + 1)], qf[i], s_out);
+        oacc[i >> 1] = mfma32x32x16(vf[i % (V_AHEAD + 1)], p_in[i & 1], oacc[i >> 1]);
       }
       // softmax, part 2: P packed to bf16 in the PV operand order, fp32 row sum
       float ls = 0.0f;
@@ -419,16 +420,18 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       lsum = __builtin_fmaf(lsum, alpha, ls);
       // keep the exponentials in this step's block (not sunk into the next one)
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
-      // schedule: the first LDS_AHEAD pairs' fragments, then per MFMA pair: MFMA, 4 VALU,
-      // MFMA, 4 VALU, the 3 LDS reads of the pair LDS_AHEAD ahead
-      __builtin_amdgcn_sched_group_barrier(0x100, 3 * LDS_AHEAD, 0);
+      // schedule: the first pairs' fragments, then per MFMA pair: MFMA, 4 VALU, MFMA, 4 VALU,
+      // the LDS reads of the pairs K_AHEAD / V_AHEAD ahead
+      __builtin_amdgcn_sched_group_barrier(0x100, K_AHEAD + 2 * V_AHEAD, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        if (i + LDS_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // 3 LDS reads
+        if (i + K_AHEAD < 8 && i + V_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        else if (i + V_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        else if (i + K_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       pend = move;
       alpha_p = alpha;
