@@ -365,6 +365,12 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       vf[i % (V_AHEAD + 1)] = u32x4{v0[0], v0[1], v1[0], v1[1]};
     };
 
+    // S of sub-block 0 (tile 0, rows 0..31)
+    if (wave_active) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
+    }
+
     // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow and,
     // for fp8, block scales sk / sv) into p_out, O += V^T p_in^T from LDS offset VO,
     // s_out = K Q^T from LDS offset KO.
