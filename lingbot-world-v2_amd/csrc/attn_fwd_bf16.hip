@@ -94,6 +94,18 @@ __device__ __forceinline__ void wait_tiles_outstanding(int n) {
   else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 
+// Materialises a kernel argument in a scalar register at this point. Its scalar load is then
+// waited for here, before the main loop: a scalar load still pending inside the loop (scalar
+// loads complete out of order) turns every LDS wait there into a wait for all LDS reads.
+__device__ __forceinline__ float sreg(float x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+__device__ __forceinline__ int sreg(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
 // Hides a value from the optimiser (keeps a base register from being re-associated with
 // constant offsets that would no longer fit the 16-bit LDS immediate).
 __device__ __forceinline__ int opaque(int x) {
@@ -112,19 +124,6 @@ __device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int 
     if (key >= mrow) sc[r] += add;
     if (key < tvlo || key >= tvhi) sc[r] = -INFINITY;
   }
-}
-
-// Packed per-tile row info: valid rows [vlo, vhi) and the first row carrying the
-// multiplicity bias (every key from a.mult_key on does; 255: none), from the cursor's tile.
-__device__ __forceinline__ int tile_rows(const AttnKernelArgs& a, const TileCursor& cs) {
-  int tvlo, tvhi;
-  cursor_rows(cs, tvlo, tvhi);
-  int mrow = 255;
-  if (a.mult_key >= 0) {
-    const int64_t r = a.mult_key - (a.seg[cs.seg].start + cs.lt * BN);
-    if (r < tvhi) mrow = r > tvlo ? (int)r : tvlo;
-  }
-  return tvlo | (tvhi << 8) | (mrow << 16);
 }
 
 __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
@@ -226,10 +225,13 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
   float m_used = -INFINITY, m_true = -INFINITY, lsum = 0.0f;  // exponent ref, row max, row sum
   const float c = a.scale_log2;
+  const float mult_raw = sreg(a.mult_raw);
+  // the call carries a multiplicity bias (mult_key >= 0: the sign of its high word)
+  const int mult = sreg((int)(a.mult_key >> 32)) >= 0;
   const float tau_raw = TAU / c;
 
   // DMA of the cursor's tile into a stage (2*NDMA x 16 B per lane); returns the tile's row
-  // info (tile_rows). Full tiles use the per-segment lane offsets; in a partial
+  // info (pack_rows). Full tiles use the per-segment lane offsets; in a partial
   // tile, rows outside the valid range fetch a valid row instead: their scores are masked to
   // -inf and their probabilities are exactly 0, so the duplicate never contributes.
   TileCursor cs;
@@ -237,36 +239,33 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   auto seg_offsets = [&]() {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
-      lane_k[i] = (uint32_t)(dma_row[i] * cs.ks + dma_col[i]);
-      lane_v[i] = (uint32_t)(dma_row[i] * cs.vs + dma_col[i]);
+      lane_k[i] = (uint32_t)dma_row[i] * cs.ks + dma_col[i];
+      lane_v[i] = (uint32_t)dma_row[i] * cs.vs + dma_col[i];
     }
   };
   const uint32_t lds_wave = lds_addr(lds) + 1024 * NDMA * wave;  // this wave's 1 KB blocks
   auto issue = [&](int stage) -> int {
-    const int rows = tile_rows(a, cs);
-    const int tvlo = rows & 0xff, tvhi = (rows >> 8) & 0xff;
-    const int64_t row0 = cs.lt * BN;
-    const unsigned char* kb = cs.kbase + row0 * cs.ks;
-    const unsigned char* vb = cs.vbase + row0 * cs.vs;
-    const uint32_t kdst = lds_wave + stage * TILE_B;
+    const int rows = cs.rows;
+    // (the base is re-materialised per call so that the per-stage addresses are not all kept live)
+    const uint32_t kdst = (uint32_t)sreg((int)lds_wave) + stage * TILE_B;
     const uint32_t vdst = kdst + V_BASE;
-    if (tvlo == 0 && tvhi == BN) {
+    if ((rows & 0xffff) == (BN << 8)) {  // every row valid
 #pragma unroll
       for (int i = 0; i < NDMA; ++i) {
-        dma16(kb, lane_k[i], kdst + 1024 * i);
-        dma16(vb, lane_v[i], vdst + 1024 * i);
+        dma16(cs.kt, lane_k[i], kdst + 1024 * i);
+        dma16(cs.vt, lane_v[i], vdst + 1024 * i);
       }
     } else {
-      const int rhi = tvhi - 1;
+      const int tvlo = rows & 0xff, rhi = ((rows >> 8) & 0xff) - 1;
 #pragma unroll
       for (int i = 0; i < NDMA; ++i) {
         int r = dma_row[i];
         r = r < tvlo ? tvlo : (r > rhi ? rhi : r);
-        dma16(kb, (uint32_t)(r * cs.ks) + dma_col[i], kdst + 1024 * i);
-        dma16(vb, (uint32_t)(r * cs.vs) + dma_col[i], vdst + 1024 * i);
+        dma16(cs.kt, (uint32_t)r * cs.ks + dma_col[i], kdst + 1024 * i);
+        dma16(cs.vt, (uint32_t)r * cs.vs + dma_col[i], vdst + 1024 * i);
       }
     }
-    if (cursor_next<ESZ>(a, lo, hi, b, h, cs) && cs.seg < a.nseg) seg_offsets();
+    if (cursor_next<ESZ>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets();
     return rows;
   };
 
@@ -276,16 +275,15 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   u32x4 k8 = {0u, 0u, 0u, 0u}, v8 = {0u, 0u, 0u, 0u};
   float sk_n = 1.0f, sv_n = 1.0f;
   auto issue8 = [&]() -> int {
-    const int rows = tile_rows(a, cs);
+    const int rows = cs.rows;
     const int tvlo = rows & 0xff, tvhi = (rows >> 8) & 0xff;
-    const int64_t row0 = cs.lt * BN;
     int r = row8;
     r = r < tvlo ? tvlo : (r > tvhi - 1 ? tvhi - 1 : r);
-    k8 = *reinterpret_cast<const u32x4*>(cs.kbase + (row0 + r) * cs.ks + 16 * j8);
-    v8 = *reinterpret_cast<const u32x4*>(cs.vbase + (row0 + r) * cs.vs + 16 * j8);
-    sk_n = cs.ksc[cs.lt];
-    sv_n = cs.vsc[cs.lt];
-    cursor_next<1>(a, lo, hi, b, h, cs);
+    k8 = *reinterpret_cast<const u32x4*>(cs.kt + (uint32_t)r * cs.ks + 16 * j8);
+    v8 = *reinterpret_cast<const u32x4*>(cs.vt + (uint32_t)r * cs.vs + 16 * j8);
+    sk_n = *cs.ksc;
+    sv_n = *cs.vsc;
+    cursor_next<1>(a, lo, hi, b, h, mult, cs);
     return rows;
   };
   auto write8 = [&](int stage) {
@@ -311,7 +309,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     int vr[NSTAGE];  // valid rows of tiles u .. u+NSTAGE-1 (u = the tile being softmaxed)
     float skr[NSTAGE], svr[NSTAGE];  // fp8 block scales of the same tiles
 #pragma unroll
-    for (int k = 0; k < NSTAGE; ++k) { vr[k] = (BN << 8) | (255 << 16); skr[k] = 1.0f; svr[k] = 1.0f; }
+    for (int k = 0; k < NSTAGE; ++k) { vr[k] = ROWS_FULL; skr[k] = 1.0f; svr[k] = 1.0f; }
     cursor_init<ESZ>(a, lo, hi, t0, b, h, cs);
     if constexpr (FP8) {
 #pragma unroll
@@ -382,8 +380,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       for (int i = 0; i < V_AHEAD; ++i) load_v(voff_c, i);
       if (pend) scale_acc(oacc, alpha_p);
       const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
-      if (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32)
-        mask_scores(s_in, kb, vlo, vhi, hl, mrow, a.mult_raw);
+      if (vrow != ROWS_FULL && (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32))
+        mask_scores(s_in, kb, vlo, vhi, hl, mrow, mult_raw);
       // softmax, part 1: running max and exponent reference (wave-uniform decision); fp8
       // scores are q . k_code, the true score is that times the K block scale
       float mx = s_in[0];

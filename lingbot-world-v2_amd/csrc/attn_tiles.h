@@ -14,15 +14,6 @@ constexpr int D = 128;
 constexpr int BN = 64;
 constexpr float TAU = 8.0f;  // lazy-rescale threshold, log2 units
 
-struct TileInfo {
-  const unsigned char* kbase;  // row 0 of the segment for (b, h)
-  const unsigned char* vbase;
-  int64_t ks, vs;              // row strides in bytes
-  int64_t row0;                // first segment-local row of the tile
-  int vlo, vhi;                // valid rows of the tile
-  float sk, sv;                // fp8 block scales
-};
-
 __device__ __forceinline__ int seg_tiles(const SegDesc& s, int64_t lo, int64_t hi, int64_t& la,
                                          int64_t& lb) {
   if (s.len <= 0) return 0;
@@ -45,72 +36,66 @@ __device__ __forceinline__ int count_tiles(const AttnKernelArgs& a, int64_t lo, 
   return n;
 }
 
-template <int ESZ, bool SCALES>
-__device__ __forceinline__ TileInfo tile_info(const AttnKernelArgs& a, int64_t lo, int64_t hi,
-                                              int g, int b, int h) {
-  // Find the segment holding tile g (uniform loop: descriptors are read on demand).
-  int cum = 0, i = 0;
-  int64_t la = 0, lb = 0;
-#pragma unroll 1
-  for (; i < a.nseg - 1; ++i) {
-    const int n = seg_tiles(a.seg[i], lo, hi, la, lb);
-    if (g < cum + n) break;
-    cum += n;
-  }
-  const SegDesc& s = a.seg[i];
-  seg_tiles(s, lo, hi, la, lb);
-  TileInfo ti;
-  const int64_t lt = la / BN + (g - cum);
-  constexpr int esz = ESZ;
-  ti.kbase = reinterpret_cast<const unsigned char*>(s.k) + (s.ksb * b + s.ksh * h) * esz;
-  ti.vbase = reinterpret_cast<const unsigned char*>(s.v) + (s.vsb * b + s.vsh * h) * esz;
-  ti.ks = s.ksl * esz;
-  ti.vs = s.vsl * esz;
-  ti.row0 = lt * BN;
-  const int64_t vlo = la - ti.row0, vhi = lb - ti.row0;
-  ti.vlo = vlo > 0 ? (int)vlo : 0;
-  ti.vhi = vhi < BN ? (int)vhi : BN;
-  if constexpr (SCALES) {
-    const int64_t bi = ((int64_t)b * a.H + h) * s.nblk + lt;
-    ti.sk = s.ks[bi];
-    ti.sv = s.vs[bi];
-  } else {
-    ti.sk = 1.0f;
-    ti.sv = 1.0f;
-  }
-  return ti;
+// Packed valid rows of a tile: rows [vlo, vhi) hold keys of the window, rows from mrow on carry
+// the multiplicity bias (255: none). ROWS_FULL: every row valid, no bias.
+__host__ __device__ constexpr int pack_rows(int vlo, int vhi, int mrow) {
+  return vlo | (vhi << 8) | (mrow << 16);
 }
+constexpr int ROWS_FULL = pack_rows(0, BN, 255);
 
-// Sequential walk over the tiles of [lo, hi), in order. The segment descriptors (kernel
-// arguments) are read only when the walk enters a new segment, so stepping to the next tile
-// is a handful of scalar instructions.
+// Sequential walk over the tiles of [lo, hi), in order. Stepping to the next tile of the same
+// segment advances two tile pointers; only the first and last tile of a segment (and every tile
+// of a call with a multiplicity bias) recompute their valid rows, and only entering a new segment
+// reads its descriptor. Segment-local indices are 32-bit (the host limits segments to 2^30 keys).
 struct TileCursor {
-  int seg;                    // current segment; nseg when the walk is past the last tile
-  int64_t lt, lt_end;         // current and one-past-last local tile of the segment
-  int64_t la, lb;             // valid local key range of the segment
-  const unsigned char* kbase; // row 0 of the segment for (b, h)
-  const unsigned char* vbase;
-  int64_t ks, vs;             // row strides in bytes
-  const float* ksc;           // fp8 block scales of (b, h) (fp8 cache only)
+  const unsigned char* kt;  // row 0 of the current tile, K and V, for (b, h)
+  const unsigned char* vt;
+  const float* ksc;         // fp8 block scales of the current tile (fp8 cache only)
   const float* vsc;
+  uint32_t kstep, vstep;    // bytes per tile (BN rows; the host keeps them below 4 GiB)
+  uint32_t ks, vs;          // row strides in bytes
+  int seg;                  // current segment; nseg when the walk is past the last tile
+  int lt, lt_end;           // current and one-past-last local tile of the segment
+  int la, lb;               // valid local key range of the segment
+  int rows;                 // packed valid rows of the current tile (pack_rows)
 };
+
+// Valid rows of the cursor's tile and, when mult_key >= 0, the first row of the keys that stand
+// for several identical keys.
+__device__ __forceinline__ int cursor_rows(const AttnKernelArgs& a, const TileCursor& c) {
+  const int row0 = c.lt * BN;
+  const int l = c.la - row0, u = c.lb - row0;
+  const int vlo = l > 0 ? l : 0;
+  const int vhi = u < BN ? u : BN;
+  int mrow = 255;
+  if (a.mult_key >= 0) {
+    const int64_t r = a.mult_key - (a.seg[c.seg].start + row0);
+    if (r < vhi) mrow = r > vlo ? (int)r : vlo;
+  }
+  return pack_rows(vlo, vhi, mrow);
+}
 
 template <int ESZ>
 __device__ __forceinline__ void cursor_enter(const AttnKernelArgs& a, int i, int64_t la,
-                                             int64_t lb, int b, int h, TileCursor& c) {
+                                             int64_t lb, int b, int h, int lt, TileCursor& c) {
   const SegDesc& s = a.seg[i];
   c.seg = i;
-  c.la = la;
-  c.lb = lb;
-  c.lt = la / BN;
-  c.lt_end = (lb + BN - 1) / BN;
-  c.kbase = reinterpret_cast<const unsigned char*>(s.k) + (s.ksb * b + s.ksh * h) * ESZ;
-  c.vbase = reinterpret_cast<const unsigned char*>(s.v) + (s.vsb * b + s.vsh * h) * ESZ;
-  c.ks = s.ksl * ESZ;
-  c.vs = s.vsl * ESZ;
-  const int64_t so = ((int64_t)b * a.H + h) * s.nblk;
+  c.la = (int)la;
+  c.lb = (int)lb;
+  c.lt = lt;
+  c.lt_end = (int)((lb + BN - 1) / BN);
+  c.ks = (uint32_t)(s.ksl * ESZ);
+  c.vs = (uint32_t)(s.vsl * ESZ);
+  c.kstep = (uint32_t)(s.ksl * ESZ * BN);
+  c.vstep = (uint32_t)(s.vsl * ESZ * BN);
+  c.kt = reinterpret_cast<const unsigned char*>(s.k) + (s.ksb * b + s.ksh * h) * ESZ +
+         (int64_t)lt * c.kstep;
+  c.vt = reinterpret_cast<const unsigned char*>(s.v) + (s.vsb * b + s.vsh * h) * ESZ +
+         (int64_t)lt * c.vstep;
+  const int64_t so = ((int64_t)b * a.H + h) * s.nblk + lt;
   c.ksc = s.ks != nullptr ? s.ks + so : nullptr;
   c.vsc = s.vs != nullptr ? s.vs + so : nullptr;
+  c.rows = cursor_rows(a, c);
 }
 
 // Positions the cursor on tile g of the walk (the g-th tile holding keys of [lo, hi)).
@@ -124,37 +109,38 @@ __device__ __forceinline__ void cursor_init(const AttnKernelArgs& a, int64_t lo,
     int64_t la = 0, lb = 0;
     const int n = seg_tiles(a.seg[i], lo, hi, la, lb);
     if (g < cum + n) {
-      cursor_enter<ESZ>(a, i, la, lb, b, h, c);
-      c.lt += g - cum;
+      cursor_enter<ESZ>(a, i, la, lb, b, h, (int)(la / BN) + g - cum, c);
       return;
     }
     cum += n;
   }
 }
 
-// Advances to the next tile; returns true when the cursor entered a new segment.
+// Advances to the next tile; returns true when the cursor entered a new segment (or ran past
+// the last one). `mult` (kernel-uniform, nonzero): the call carries a multiplicity bias.
 template <int ESZ>
 __device__ __forceinline__ bool cursor_next(const AttnKernelArgs& a, int64_t lo, int64_t hi,
-                                            int b, int h, TileCursor& c) {
-  if (++c.lt < c.lt_end) return false;
+                                            int b, int h, int mult, TileCursor& c) {
+  if (++c.lt < c.lt_end) {
+    c.kt += c.kstep;
+    c.vt += c.vstep;
+    if constexpr (ESZ == 1) {
+      ++c.ksc;
+      ++c.vsc;
+    }
+    c.rows = (c.lt + 1 < c.lt_end && !mult) ? ROWS_FULL : cursor_rows(a, c);
+    return false;
+  }
 #pragma unroll 1
   for (int i = c.seg + 1; i < a.nseg; ++i) {
     int64_t la = 0, lb = 0;
     if (seg_tiles(a.seg[i], lo, hi, la, lb) > 0) {
-      cursor_enter<ESZ>(a, i, la, lb, b, h, c);
+      cursor_enter<ESZ>(a, i, la, lb, b, h, (int)(la / BN), c);
       return true;
     }
   }
   c.seg = a.nseg;
   return true;
-}
-
-// Valid rows [vlo, vhi) of the cursor's tile.
-__device__ __forceinline__ void cursor_rows(const TileCursor& c, int& vlo, int& vhi) {
-  const int64_t row0 = c.lt * BN;
-  const int64_t l = c.la - row0, u = c.lb - row0;
-  vlo = l > 0 ? (int)l : 0;
-  vhi = u < BN ? (int)u : BN;
 }
 
 }  // namespace lbw

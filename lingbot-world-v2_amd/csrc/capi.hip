@@ -157,6 +157,9 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   for (int i = 0; i < p->n_segments; ++i) {
     const lbw_kv_segment& s = p->seg[i];
     if (s.len < 0) return fail(LBW_ERR_INVALID, "segment %d: negative length", i);
+    // the kernels index keys within a segment with 32-bit integers
+    if (s.len > (int64_t(1) << 30))
+      return fail(LBW_ERR_UNSUPPORTED, "segment %d: more than 2^30 keys", i);
     if (s.len > 0) {
       if (s.k == nullptr || s.v == nullptr || !aligned16(s.k) || !aligned16(s.v))
         return fail(LBW_ERR_INVALID, "segment %d: k/v must be 16-byte aligned device pointers", i);

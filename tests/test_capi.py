@@ -103,6 +103,28 @@ def _split_count(H, LQ, LK):
     return n // (LQ * H * 130 * 4)
 
 
+def test_segment_length_limit_without_gpu():
+    """Segments longer than 2^30 keys are refused before any HIP call (32-bit key indices)."""
+    from lbw_amd import _lib
+    lib = _lib.load()
+    p = _lib.AttnParams()
+    p.batch, p.heads, p.head_dim, p.lq = 1, 1, 128, 4
+    p.q = p.out = 256
+    p.q_stride_b = p.o_stride_b = 4 * 128
+    p.q_stride_l = p.o_stride_l = 128
+    p.q_stride_h = p.o_stride_h = 128
+    p.n_segments = 1
+    s = p.seg[0]
+    s.k = s.v = 256
+    s.len = (1 << 30) + 1
+    s.k_stride_l = s.v_stride_l = 128
+    s.k_stride_b = s.v_stride_b = s.len * 128
+    s.k_stride_h = s.v_stride_h = 128
+    p.kv_lo, p.kv_hi = 0, -1
+    assert lib.lbw_attention_fwd(ctypes.byref(p), None, 0, None) == 2
+    assert b"2^30" in lib.lbw_last_error()
+
+
 def test_split_plan_for_the_measured_shapes():
     """The split heuristic's choices for the shapes it was fitted on (gfx950, 256 CUs): 14B
     720p (3 splits), 14B 480p and 1.3B 480p 3-frame chunks (single pass), 1.3B one frame (3)."""
