@@ -115,14 +115,21 @@ __device__ __forceinline__ int opaque(int x) {
 
 // Scores of keys outside the tile's valid rows [tvlo, tvhi) -> -inf (S^T register layout);
 // rows from mrow on get `add` (the log-multiplicity of deduplicated keys).
+// Sign-bit arithmetic on per-lane integers instead of one comparison mask per element: the
+// sixteen 64-bit lane masks would otherwise all be live in scalar registers at once.
 __device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int tvhi, int hl,
                                             int mrow, float add) {
   asm volatile("" ::: "memory");
+  const int k0 = 32 * kb + 4 * hl;  // key of register 0 in this lane
+  const int a = k0 - tvlo, bnd = tvhi - 1 - k0, cm = k0 - mrow;
+  const uint32_t addb = __float_as_uint(add);
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const int key = 32 * kb + 8 * (r >> 2) + 4 * hl + (r & 3);
-    if (key >= mrow) sc[r] += add;
-    if (key < tvlo || key >= tvhi) sc[r] = -INFINITY;
+    const int o = 8 * (r >> 2) + (r & 3);              // key - k0 of register r
+    const uint32_t out = (uint32_t)(((a + o) | (bnd - o)) >> 31);  // ~0: key outside [tvlo, tvhi)
+    const uint32_t biased = ~(uint32_t)((cm + o) >> 31);           // ~0: key >= mrow
+    const float x = sc[r] + __uint_as_float(addb & biased);
+    sc[r] = __uint_as_float((__float_as_uint(x) & ~out) | (0xff800000u & out));
   }
 }
 
@@ -223,7 +230,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   for (int db = 0; db < 4; ++db)
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
-  float m_used = -INFINITY, m_true = -INFINITY, lsum = 0.0f;  // exponent ref, row max, row sum
+  float m_used = M_INIT, m_true = -INFINITY, lsum = 0.0f;  // exponent ref, row max, row sum
   const float c = a.scale_log2;
   const float mult_raw = sreg(a.mult_raw);
   // the call carries a multiplicity bias (mult_key >= 0: the sign of its high word)
@@ -382,19 +389,29 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
       if (vrow != ROWS_FULL && (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32))
         mask_scores(s_in, kb, vlo, vhi, hl, mrow, mult_raw);
-      // softmax, part 1: running max and exponent reference (wave-uniform decision); fp8
-      // scores are q . k_code, the true score is that times the K block scale
-      float mx = s_in[0];
+      // softmax, part 1: running max and exponent reference (wave-uniform decision)
+      if constexpr (FP8) {
+        // fp8 scores are q . k_code; the true score is that times the K block scale
+        float mx = s_in[0];
 #pragma unroll
-      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
-      mx = wave_max_xor32(mx);
-      if constexpr (FP8) mx *= sk;
-      m_true = fmaxf(m_true, mx);
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+        m_true = fmaxf(m_true, wave_max_xor32(mx) * sk);
+      } else {
+        // lanes l and l^32 hold the same query's running max: fold it in before the exchange
+        float mx = m_true;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+        m_true = wave_max_xor32(mx);
+      }
+      // The reference starts at M_INIT, a finite stand-in for -inf, so no step needs an
+      // infinity case: the first valid score moves it (alpha = exp2(-huge) = 0 scales the empty
+      // accumulators), masked scores (-inf) give p = 0. Every lane sees the same valid keys, so
+      // m_true is -inf in all lanes or in none, and a move never selects -inf.
       const bool move = __any(m_true > m_used + tau_raw);
       const float m_new = move ? m_true : m_used;
-      const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2((m_used - m_new) * c);
+      const float alpha = fast_exp2((m_used - m_new) * c);
       m_used = m_new;
-      const float mc = m_used == -INFINITY ? 0.0f : m_used * c;
+      const float mc = m_new * c;
       // p = exp2(s_code sk c - m c), times sv for fp8 (V's scale, so that P^T V_code = P^T V)
       const float cm = FP8 ? c * sk : c;
       const float ca = FP8 ? __builtin_amdgcn_logf(sv) - mc : -mc;
@@ -409,7 +426,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         oacc[i >> 1] = mfma32x32x16(vf[i % (V_AHEAD + 1)], p_in[i & 1], oacc[i >> 1]);
       }
       // softmax, part 2: P packed to bf16 in the PV operand order, fp32 row sum
-      float ls = 0.0f;
+      float ls;
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
 #pragma unroll
@@ -417,7 +434,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], cm, ca));
           const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], cm, ca));
           p_out[m][e] = pack_bf16x2(x0, x1);
-          ls += x0 + x1;
+          ls = (m == 0 && e == 0) ? x0 + x1 : ls + (x0 + x1);
         }
       }
       if constexpr (FP8) ls *= __builtin_amdgcn_rcpf(sv);
@@ -425,7 +442,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       // keep the exponentials in this step's block (not sunk into the next one)
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
       // schedule: the first pairs' fragments, then per MFMA pair: MFMA, 4 VALU, MFMA, 4 VALU,
-      // the LDS reads of the pairs K_AHEAD / V_AHEAD ahead
+      // the LDS reads of the pairs K_AHEAD / V_AHEAD ahead (the VALU work spread over the
+      // whole step measured faster than larger groups that finish it early)
       __builtin_amdgcn_sched_group_barrier(0x100, K_AHEAD + 2 * V_AHEAD, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {

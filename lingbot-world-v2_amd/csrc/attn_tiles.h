@@ -13,6 +13,7 @@ namespace lbw {
 constexpr int D = 128;
 constexpr int BN = 64;
 constexpr float TAU = 8.0f;  // lazy-rescale threshold, log2 units
+constexpr float M_INIT = -1e30f;  // initial exponent reference (finite stand-in for -inf)
 
 __device__ __forceinline__ int seg_tiles(const SegDesc& s, int64_t lo, int64_t hi, int64_t& la,
                                          int64_t& lb) {
