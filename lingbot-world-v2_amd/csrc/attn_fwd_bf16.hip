@@ -356,35 +356,53 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     bool pend = false;
     float alpha_p = 1.0f;
 
-    // LDS fragments in flight: K of pair i in kf[i % (K_AHEAD + 1)], V in vf[i % (V_AHEAD + 1)]
-    u32x4 kf[K_AHEAD + 1], vf[V_AHEAD + 1];
+    // LDS fragments in flight: K of pair i in kf[i % KR], V in vf[i % VR]. The rings hold a
+    // multiple of 8 slots' worth of indices (8 % KR == 0), so the last pairs of a step can read
+    // the next step's first fragments into the slots that step expects.
+    constexpr int KR = K_AHEAD + 2, VR = V_AHEAD + 2;
+    static_assert(8 % KR == 0 && 8 % VR == 0, "fragment rings must divide 8");
+    u32x4 kf[KR], vf[VR];
     auto load_k = [&](auto ko_c, int i) {
       constexpr int KO = decltype(ko_c)::value;
-      kf[i % (K_AHEAD + 1)] = lds_read_b128(koff[i] + KO);
+      kf[i % KR] = lds_read_b128(koff[i] + KO);
     };
     auto load_v = [&](auto vo_c, int i) {
       constexpr int VO = decltype(vo_c)::value;
       const int db = i >> 1, m = i & 1;
       const u32x2 v0 = lds_read_tr16(voff[db][0] + VO + 16 * m * ROWB);
       const u32x2 v1 = lds_read_tr16(voff[db][1] + VO + 16 * m * ROWB);
-      vf[i % (V_AHEAD + 1)] = u32x4{v0[0], v0[1], v1[0], v1[1]};
+      vf[i % VR] = u32x4{v0[0], v0[1], v1[0], v1[1]};
     };
 
-    // S of sub-block 0 (tile 0, rows 0..31)
+    // S of sub-block 0 (tile 0, rows 0..31), and the first fragments of step 0: K of tile 0
+    // rows 32..63, V of the zeroed "previous sub-block"
     if (wave_active) {
 #pragma unroll
       for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
+#pragma unroll
+      for (int i = 0; i < K_AHEAD; ++i) load_k(std::integral_constant<int, HALF_B>{}, i);
+#pragma unroll
+      for (int i = 0; i < V_AHEAD; ++i)
+        load_v(std::integral_constant<int, (NSTAGE - 1) * TILE_B + HALF_B>{}, i);
     }
 
     // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow and,
     // for fp8, block scales sk / sv) into p_out, O += V^T p_in^T from LDS offset VO,
-    // s_out = K Q^T from LDS offset KO.
-    auto step = [&](auto koff_c, auto voff_c, floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2],
-                    u32x4 (&p_out)[2], int kb, int vrow, float sk, float sv) {
+    // s_out = K Q^T from LDS offset KO. KPRE / VPRE: the first K / V fragments were read by the
+    // previous step; NKO / NVO (>= 0): read the next step's first fragments from there.
+    auto step = [&](auto koff_c, auto voff_c, auto kpre_c, auto vpre_c, auto nko_c, auto nvo_c,
+                    floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2], u32x4 (&p_out)[2], int kb,
+                    int vrow, float sk, float sv) {
+      constexpr bool KPRE = decltype(kpre_c)::value, VPRE = decltype(vpre_c)::value;
+      constexpr int NKO = decltype(nko_c)::value, NVO = decltype(nvo_c)::value;
+      if constexpr (!KPRE) {
 #pragma unroll
-      for (int i = 0; i < K_AHEAD; ++i) load_k(koff_c, i);
+        for (int i = 0; i < K_AHEAD; ++i) load_k(koff_c, i);
+      }
+      if constexpr (!VPRE) {
 #pragma unroll
-      for (int i = 0; i < V_AHEAD; ++i) load_v(voff_c, i);
+        for (int i = 0; i < V_AHEAD; ++i) load_v(voff_c, i);
+      }
       if (pend) scale_acc(oacc, alpha_p);
       const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
       if (vrow != ROWS_FULL && (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32))
@@ -421,9 +439,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (i + K_AHEAD < 8) load_k(koff_c, i + K_AHEAD);
+        else if constexpr (NKO >= 0) load_k(nko_c, i + K_AHEAD - 8);
         if (i + V_AHEAD < 8) load_v(voff_c, i + V_AHEAD);
-        s_out = mfma32x32x16(kf[i % (K_AHEAD + 1)], qf[i], s_out);
-        oacc[i >> 1] = mfma32x32x16(vf[i % (V_AHEAD + 1)], p_in[i & 1], oacc[i >> 1]);
+        else if constexpr (NVO >= 0) load_v(nvo_c, i + V_AHEAD - 8);
+        s_out = mfma32x32x16(kf[i % KR], qf[i], s_out);
+        oacc[i >> 1] = mfma32x32x16(vf[i % VR], p_in[i & 1], oacc[i >> 1]);
       }
       // softmax, part 2: P packed to bf16 in the PV operand order, fp32 row sum
       float ls;
@@ -444,16 +464,18 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       // schedule: the first pairs' fragments, then per MFMA pair: MFMA, 4 VALU, MFMA, 4 VALU,
       // the LDS reads of the pairs K_AHEAD / V_AHEAD ahead (the VALU work spread over the
       // whole step measured faster than larger groups that finish it early)
-      __builtin_amdgcn_sched_group_barrier(0x100, K_AHEAD + 2 * V_AHEAD, 0);
+      constexpr int NDS0 = (KPRE ? 0 : K_AHEAD) + (VPRE ? 0 : 2 * V_AHEAD);
+      if constexpr (NDS0 > 0) __builtin_amdgcn_sched_group_barrier(0x100, NDS0, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        if (i + K_AHEAD < 8 && i + V_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-        else if (i + V_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        else if (i + K_AHEAD < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        const bool rk = i + K_AHEAD < 8 || NKO >= 0, rv = i + V_AHEAD < 8 || NVO >= 0;
+        if (rk && rv) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        else if (rv) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        else if (rk) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       }
       pend = move;
       alpha_p = alpha;
@@ -470,9 +492,13 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       constexpr int SN = (ST + 1) % NSTAGE;           // stage of tile u+1
       const int vrow = vr[0];
       const float sk = skr[0], sv = svr[0];
+      // step 2u reads the V fragments of step 2u+1 (tile u, already resident); step 2u+1 reads
+      // those of step 2u+2 (tile u+1 rows 32..63, resident since the barrier, and tile u)
       if (wave_active)
         step(std::integral_constant<int, ST * TILE_B + HALF_B>{},
-             std::integral_constant<int, SP * TILE_B + HALF_B>{}, sA, sB, pA, pB, 0, vrow, sk, sv);
+             std::integral_constant<int, SP * TILE_B + HALF_B>{}, std::true_type{},
+             std::true_type{}, std::integral_constant<int, -1>{},
+             std::integral_constant<int, ST * TILE_B>{}, sA, sB, pA, pB, 0, vrow, sk, sv);
       if constexpr (FP8) {
         // tile u+1 (loaded one tile ago) into its stage, the one tile u-2 left
         if (u >= 1 && u + 1 < T) write8(SN);
@@ -492,7 +518,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
       if (wave_active)
         step(std::integral_constant<int, SN * TILE_B>{},
-             std::integral_constant<int, ST * TILE_B>{}, sB, sA, pB, pA, 1, vrow, sk, sv);
+             std::integral_constant<int, ST * TILE_B>{}, std::false_type{}, std::true_type{},
+             std::integral_constant<int, SN * TILE_B + HALF_B>{},
+             std::integral_constant<int, ST * TILE_B + HALF_B>{}, sB, sA, pB, pA, 1, vrow, sk, sv);
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k) {
         vr[k] = vr[k + 1];
