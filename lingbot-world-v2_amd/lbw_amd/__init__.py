@@ -8,7 +8,8 @@ when it is missing.
 from .attention import (attention, attention_merge, attention_partial, attention_segments,
                         cross_attention, exact_attention, exact_attention_chunks,
                         flash_attention, padding_start)
-from .chunked_kv_cache import FlatKVCache, allocate_self_kv_chunks, chunk_routing, num_chunks
+from .chunked_kv_cache import (FlatKVCache, allocate_self_kv_chunks, allocate_self_kv_chunks_fp8,
+                               chunk_routing, num_chunks)
 from .fp8 import Fp8KV, attention_fp8kv, quantize_kv_fp8
 from .layer import WanCrossAttention, WanSelfAttention
 from .qk_post import qk_norm_rope, qk_norm_rope_
@@ -19,6 +20,6 @@ __all__ = [
     "cross_attention", "padding_start", "attention_partial", "attention_merge", "attention_segments",
     "qk_norm_rope", "qk_norm_rope_", "RopeTables", "causal_rope_tables", "rope_params",
     "wan_rope_freqs", "Fp8KV", "quantize_kv_fp8", "attention_fp8kv", "FlatKVCache",
-    "allocate_self_kv_chunks", "chunk_routing", "num_chunks", "WanSelfAttention",
+    "allocate_self_kv_chunks", "allocate_self_kv_chunks_fp8", "chunk_routing", "num_chunks", "WanSelfAttention",
     "WanCrossAttention",
 ]

@@ -13,7 +13,8 @@ from dataclasses import dataclass
 
 import torch
 
-__all__ = ["num_chunks", "chunk_routing", "allocate_self_kv_chunks", "ordered_chunks",
+__all__ = ["num_chunks", "chunk_routing", "allocate_self_kv_chunks",
+           "allocate_self_kv_chunks_fp8", "ordered_chunks",
            "ordered_chunks_by_block", "chunk_bytes", "FlatWritePlan", "plan_flat_write",
            "FlatKVCache"]
 
@@ -54,6 +55,31 @@ def allocate_self_kv_chunks(num_layers, batch, chunk_tokens, heads, head_dim, n_
               for _ in range(n_chunks)]
         cache.append({"k": ks, "v": vs})
     return cache
+
+
+def allocate_self_kv_chunks_fp8(num_layers, batch, chunk_tokens, heads, head_dim, n_chunks,
+                                device="cuda"):
+    """fp8-e4m3 variant of :func:`allocate_self_kv_chunks` (no reference counterpart): per
+    layer ``n_chunks`` K and V slots of uint8 codes ``[B, chunk_tokens, N, D]`` with fp32
+    scales ``[B, N, ceil(chunk_tokens / 64)]`` (``lbw_amd.fp8.Fp8KV``; an all-zero slot has
+    codes 0 and scales 1), plus one bf16 staging pair ``[B, chunk_tokens, N, D]`` shared by
+    the layers: the fused q/k kernel commits the chunk's roped K and V there and the quantiser
+    turns them into the destination slot. Each slot is its own KV segment, so scale blocks
+    start at the slot's first token and a 64-token block never straddles two chunks."""
+    from .fp8 import BLOCK, Fp8KV
+    nblk = (chunk_tokens + BLOCK - 1) // BLOCK
+
+    def slot():
+        return Fp8KV(torch.zeros(batch, chunk_tokens, heads, head_dim, dtype=torch.uint8,
+                                 device=device),
+                     torch.ones(batch, heads, nblk, dtype=torch.float32, device=device))
+
+    stage = {"k": torch.zeros(batch, chunk_tokens, heads, head_dim, dtype=torch.bfloat16,
+                              device=device),
+             "v": torch.zeros(batch, chunk_tokens, heads, head_dim, dtype=torch.bfloat16,
+                              device=device)}
+    return [{"k": [slot() for _ in range(n_chunks)], "v": [slot() for _ in range(n_chunks)],
+             "stage": stage} for _ in range(num_layers)]
 
 
 def ordered_chunks(block_cache, destination, leading):

@@ -52,8 +52,10 @@ def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softma
                     num_splits: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
     """Attention of bf16 q ``[B, Lq, N, 128]`` over fp8 segments ``[(Fp8KV k, Fp8KV v), ...]``.
 
-    Q is quantised per query row inside the kernel; QK^T runs on the fp8 MFMA with the
-    K block scales folded into the softmax exponent; V is dequantised on its way to LDS."""
+    The kernel converts each 64-token tile's codes exactly to bf16 on their way to LDS (every
+    e4m3 value is a bf16 value) and runs the bf16 MFMA loop with q unquantised; the K block
+    scale folds into the softmax exponent's multiplier and the V block scale into its addend
+    (and out of the row sum)."""
     lib = _lib.load()
     device = q.device
     _check_4d("q", q, device)

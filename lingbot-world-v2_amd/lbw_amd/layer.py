@@ -18,6 +18,7 @@ import torch.nn.functional as F
 
 from .attention import attention_segments, cross_attention, padding_start
 from .chunked_kv_cache import FlatKVCache, chunk_routing, ordered_chunks
+from .fp8 import attention_fp8kv, quantize_kv_fp8
 from .qk_post import qk_norm_rope_
 from .rope import RopeTables, causal_rope_tables, wan_rope_freqs
 
@@ -97,6 +98,28 @@ class WanSelfAttention:
                                     vd[0].view(L, self.C))
         kk, vv = ordered_chunks(chunks, dest, leading)
         o = attention_segments(q.view(1, L, self.heads, self.head_dim), list(zip(kk, vv)))
+        return F.linear(o.view(1, L, self.C), self.wo, self.bo)
+
+
+    def forward_chunked_fp8(self, x, grid, start_frame, chunks, chunk_index: int):
+        """forward_chunked over an fp8-e4m3 chunked cache (allocate_self_kv_chunks_fp8): the
+        fused kernel commits the chunk's roped K and V in bf16 to the staging pair, the
+        quantiser writes codes + block scales into the routed slot (a second pass: the block
+        scales need the amax of 64 tokens x 128 features per head, which the row-parallel q/k
+        kernel does not see at once), and the attention reads the fp8 slots with bf16 q."""
+        L = x.shape[1]
+        n = len(chunks["k"])
+        dest, leading = chunk_routing(chunk_index, n)
+        kd, vd = chunks["k"][dest], chunks["v"][dest]
+        if kd.codes.shape[1] != L:
+            raise ValueError(f"chunk slots hold {kd.codes.shape[1]} tokens, the chunk has {L}")
+        sk, sv = chunks["stage"]["k"], chunks["stage"]["v"]
+        q = self._project_norm_rope(x, grid, start_frame, sk[0].view(L, self.C),
+                                    sv[0].view(L, self.C))
+        quantize_kv_fp8(sk, out=kd)
+        quantize_kv_fp8(sv, out=vd)
+        kk, vv = ordered_chunks(chunks, dest, leading)
+        o = attention_fp8kv(q.view(1, L, self.heads, self.head_dim), list(zip(kk, vv)))
         return F.linear(o.view(1, L, self.C), self.wo, self.bo)
 
 

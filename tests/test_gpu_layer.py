@@ -83,6 +83,34 @@ def test_chunked_cache_path_equals_flat(lib):
         assert m["nonfinite"] == 0 and m["max_abs"] <= 1e-3, (i, m)
 
 
+def test_chunked_fp8_cache_path(lib):
+    """The fp8 chunked cache: the routed slot holds exactly quantize_kv_fp8 of the chunk's
+    roped K/V (the bf16 chunked cache's slot), and the layer output stays within the fp8
+    tolerance (cosine >= 0.999) of the bf16 chunked path, over 4 chunks so that slot 1 is
+    rewritten and the sink stays."""
+    from lbw_amd import (WanSelfAttention, allocate_self_kv_chunks, allocate_self_kv_chunks_fp8,
+                         quantize_kv_fp8)
+    g = torch.Generator().manual_seed(4)
+    C, H, F = 512, 4, 8 * 8
+    ws = _weights(C, g, 0.02, 0.05)
+    layer = _layer(WanSelfAttention, ws, H)
+    frames = [torch.randn(1, F, C, generator=g).to(torch.bfloat16).to(DEV) for _ in range(4)]
+    bf = allocate_self_kv_chunks(1, 1, F, H, 128, 3, device=DEV)[0]
+    f8 = allocate_self_kv_chunks_fp8(1, 1, F, H, 128, 3, device=DEV)[0]
+    from lbw_amd import chunk_routing
+    for i, fr in enumerate(frames):
+        a = layer.forward_chunked(fr, (1, 8, 8), i, bf, chunk_index=i)
+        b = layer.forward_chunked_fp8(fr, (1, 8, 8), i, f8, chunk_index=i)
+        dest, _ = chunk_routing(i, 3)
+        for key in ("k", "v"):
+            ref = quantize_kv_fp8(bf[key][dest])
+            assert torch.equal(f8[key][dest].codes, ref.codes), (i, key)
+            assert torch.equal(f8[key][dest].scales, ref.scales), (i, key)
+        cs = cosine(b, a)
+        print(i, dest, f"cos {cs:.6f}")
+        assert torch.isfinite(b).all() and cs >= 0.999, (i, cs)
+
+
 def test_wan14b_cross_attention_layer(lib):
     """14B cross-attention: 4680 chunk queries against a 512-token context of dim 4096
     (N(0,1), rows 300..511 zeroed) projected to 5120 by N(0, 0.02) weights; masked to the

@@ -56,3 +56,16 @@ def test_allocate_and_order_chunks():
     assert C.chunk_bytes(cache) == 2 * 2 * 4 * 8 * 2 * 4 * 2
     ks, vs = C.ordered_chunks(cache[0], 2, (0, 1, 3))
     assert ks[-1] is cache[0]["k"][2] and vs[0] is cache[0]["v"][0]
+
+
+def test_allocate_fp8_chunks_layout():
+    """fp8 chunk slots: uint8 codes in the token-major layout, one fp32 scale per (batch, head,
+    64-token block of the slot), and one bf16 staging pair per layer."""
+    cache = C.allocate_self_kv_chunks_fp8(2, 1, 100, 3, 128, 4, device="cpu")
+    assert len(cache) == 2 and len(cache[0]["k"]) == 4 and len(cache[1]["v"]) == 4
+    s = cache[0]["k"][1]
+    assert s.codes.shape == (1, 100, 3, 128) and s.codes.dtype == torch.uint8
+    assert s.scales.shape == (1, 3, 2) and bool((s.scales == 1).all())
+    assert cache[0]["stage"]["v"].shape == (1, 100, 3, 128)
+    assert cache[0]["stage"]["k"].dtype == torch.bfloat16
+
