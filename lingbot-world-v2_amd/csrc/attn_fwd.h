@@ -41,6 +41,8 @@ struct AttnKernelArgs {
   float* part_l;
   int64_t mult_key;   // first of the keys that each stand for several identical keys, or -1
   float mult_raw;     // ln(multiplicity) / scale: added to those keys' raw scores
+  int track_max;      // partials must carry the true row max (cte_partial contract); otherwise
+                      // any exponent reference consistent with O and l will do
 };
 
 struct MergeKernelArgs {

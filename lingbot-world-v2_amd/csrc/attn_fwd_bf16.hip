@@ -145,7 +145,7 @@ __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
 // converted exactly to bf16 (every e4m3 value is a bf16 value) and written into the same LDS
 // layout; the block scales fold into the softmax (K's into the exponent's multiplier, V's into
 // its addend as log2, and out of the row sum), so the MFMA loop is the bf16 one.
-template <bool FP8>
+template <bool FP8, bool TRACK>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
@@ -407,32 +407,38 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
       if (vrow != ROWS_FULL && (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32))
         mask_scores(s_in, kb, vlo, vhi, hl, mrow, mult_raw);
-      // softmax, part 1: running max and exponent reference (wave-uniform decision)
-      if constexpr (FP8) {
-        // fp8 scores are q . k_code; the true score is that times the K block scale
-        float mx = s_in[0];
+      // softmax, part 1 (TRACK): running max and exponent reference, decided before the
+      // exponentials (wave-uniform). Without TRACK the exponentials use the current reference
+      // and part 3 checks them afterwards.
+      bool move = false;
+      float alpha = 1.0f;
+      if constexpr (TRACK) {
+        if constexpr (FP8) {
+          // fp8 scores are q . k_code; the true score is that times the K block scale
+          float mx = s_in[0];
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
-        m_true = fmaxf(m_true, wave_max_xor32(mx) * sk);
-      } else {
-        // lanes l and l^32 hold the same query's running max: fold it in before the exchange
-        float mx = m_true;
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+          m_true = fmaxf(m_true, wave_max_xor32(mx) * sk);
+        } else {
+          // lanes l and l^32 hold the same query's running max: fold it in before the exchange
+          float mx = m_true;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
-        m_true = wave_max_xor32(mx);
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+          m_true = wave_max_xor32(mx);
+        }
+        // Every lane sees the same valid keys, so m_true is -inf in all lanes or in none, and
+        // a move never selects -inf.
+        move = __any(m_true > m_used + tau_raw);
+        const float m_new = move ? m_true : m_used;
+        alpha = fast_exp2((m_used - m_new) * c);
+        m_used = m_new;
       }
       // The reference starts at M_INIT, a finite stand-in for -inf, so no step needs an
-      // infinity case: the first valid score moves it (alpha = exp2(-huge) = 0 scales the empty
-      // accumulators), masked scores (-inf) give p = 0. Every lane sees the same valid keys, so
-      // m_true is -inf in all lanes or in none, and a move never selects -inf.
-      const bool move = __any(m_true > m_used + tau_raw);
-      const float m_new = move ? m_true : m_used;
-      const float alpha = fast_exp2((m_used - m_new) * c);
-      m_used = m_new;
-      const float mc = m_new * c;
+      // infinity case: masked scores (-inf) give p = 0, and the first valid score moves it.
       // p = exp2(s_code sk c - m c), times sv for fp8 (V's scale, so that P^T V_code = P^T V)
       const float cm = FP8 ? c * sk : c;
-      const float ca = FP8 ? __builtin_amdgcn_logf(sv) - mc : -mc;
+      const float lsv = FP8 ? __builtin_amdgcn_logf(sv) : 0.0f;
+      float ca = lsv - m_used * c;
       // MFMAs of the neighbouring sub-blocks
 #pragma unroll
       for (int r = 0; r < 16; ++r) s_out[r] = 0.0f;
@@ -446,18 +452,41 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         oacc[i >> 1] = mfma32x32x16(vf[i % VR], p_in[i & 1], oacc[i >> 1]);
       }
       // softmax, part 2: P packed to bf16 in the PV operand order, fp32 row sum
-      float ls;
+      auto exps = [&]() {
+        float l;
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
+        for (int m = 0; m < 2; ++m) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], cm, ca));
-          const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], cm, ca));
-          p_out[m][e] = pack_bf16x2(x0, x1);
-          ls = (m == 0 && e == 0) ? x0 + x1 : ls + (x0 + x1);
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], cm, ca));
+            const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], cm, ca));
+            p_out[m][e] = pack_bf16x2(x0, x1);
+            l = (m == 0 && e == 0) ? x0 + x1 : l + (x0 + x1);
+          }
+        }
+        if constexpr (FP8) l *= __builtin_amdgcn_rcpf(sv);
+        return l;
+      };
+      float ls = exps();
+      if constexpr (!TRACK) {
+        // softmax, part 3: a row sum beyond 2^16 (or not finite) means some p outgrew the
+        // reference. Rare after a row's first tiles: move the reference to the row max of
+        // this sub-block (and the old reference), redo the exponentials, and rescale O and l
+        // by alpha like a tracked move. Exact either way: O and l share the reference.
+        if (__any(!(ls <= P_LIMIT))) {
+          float mx = s_in[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+          mx = wave_max_xor32(mx);
+          if constexpr (FP8) mx *= sk;
+          const float m_new = fmaxf(mx, m_used);
+          alpha = fast_exp2((m_used - m_new) * c);
+          m_used = m_new;
+          move = true;
+          ca = lsv - m_new * c;
+          ls = exps();
         }
       }
-      if constexpr (FP8) ls *= __builtin_amdgcn_rcpf(sv);
       lsum = __builtin_fmaf(lsum, alpha, ls);
       // keep the exponentials in this step's block (not sunk into the next one)
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
@@ -571,12 +600,17 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         }
     }
   } else {
-    // cte_partial contract: O and l relative to the true row max, m in scaled units.
+    // cte_partial contract (TRACK): O and l relative to the true row max, m in scaled units;
+    // the split-KV partials for lbw's own merge keep the exponent reference instead.
     float f = 1.0f;
     float m_out = -INFINITY;
     if (l_tot > 0.0f) {
-      f = fast_exp2((m_used - m_true) * c);
-      m_out = m_true * a.scale;
+      if constexpr (TRACK) {
+        f = fast_exp2((m_used - m_true) * c);
+        m_out = m_true * a.scale;
+      } else {
+        m_out = m_used * a.scale;
+      }
     }
     if (q < a.Lq) {
       const int64_t row = ((int64_t)(split * a.B + b) * a.H + h) * a.Lq + q;
@@ -603,22 +637,23 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-template <bool FP8>
+template <bool FP8, bool TRACK>
 static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8>,
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t nwg = (uint32_t)a.n_qtiles * a.splits * a.H * a.B;
-  hipLaunchKernelGGL(attn_fwd_bf16_kernel<FP8>, dim3(nwg), dim3(NWAVE * 64), LDS_B, stream, a);
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
+                     stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
-  return launch<false>(a, stream);
+  return a.track_max ? launch<false, true>(a, stream) : launch<false, false>(a, stream);
 }
 
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {
-  return launch<true>(a, stream);
+  return a.track_max ? launch<true, true>(a, stream) : launch<true, false>(a, stream);
 }
 
 }  // namespace lbw

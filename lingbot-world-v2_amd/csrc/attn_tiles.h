@@ -14,6 +14,7 @@ constexpr int D = 128;
 constexpr int BN = 64;
 constexpr float TAU = 8.0f;  // lazy-rescale threshold, log2 units
 constexpr float M_INIT = -1e30f;  // initial exponent reference (finite stand-in for -inf)
+constexpr float P_LIMIT = 65536.0f;  // largest per-lane row sum before the reference moves
 
 __device__ __forceinline__ int seg_tiles(const SegDesc& s, int64_t lo, int64_t hi, int64_t& la,
                                          int64_t& lb) {

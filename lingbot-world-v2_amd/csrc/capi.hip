@@ -199,6 +199,7 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   a.n_qtiles = (p->lq + bm - 1) / bm;
   a.part_o = p->part_o; a.part_m = p->part_m; a.part_l = p->part_l;
   a.mode = partials ? kModePartials : kModeNormalized;
+  a.track_max = partials ? 1 : 0;  // split partials only feed lbw's own merge
 
   // KV splits: more workgroups when (q-tiles x heads x batch) leaves the last dispatch round
   // of the CUs mostly empty. Each extra split costs one fp32 partial per query row.
