@@ -102,6 +102,35 @@ def test_split_kv_merge_matches_single_pass(lib, splits):
     assert (one.float() - many.float()).abs().max() < 4e-3
 
 
+@pytest.mark.parametrize("jump", [2.0, 12.0, 60.0])
+def test_exponent_reference_moves_mid_row(lib, jump):
+    """Scores that rise tile after tile (by `jump` natural-log units per 64-key tile along one
+    direction of q): the row maximum keeps moving, so the exponentials computed against the
+    current reference outgrow 2^16 (jump 2.0: every few tiles; 12.0: every tile, and without a
+    move they would pass fp32's range by the last tile; 60.0: they overflow to +inf at once) and
+    the step must move the reference and redo them. Against the oracle, in the single-pass and
+    the 3-split path, and through the partials (exact row max). With the redo switched off the
+    12.0 and 60.0 cases fail."""
+    from lbw_amd import attention_partial, attention_segments
+    g = torch.Generator().manual_seed(31)
+    B, Lq, H, L = 1, 70, 2, 12 * 64 + 17
+    u = torch.randn(128, generator=g)
+    u = u / u.norm()
+    q = (torch.randn(B, Lq, H, 128, generator=g) * 0.3 + 4.0 * u).to(torch.bfloat16)
+    ramp = torch.arange(L, dtype=torch.float32).div(64).floor()          # tile index per key
+    # q . k gains ~ jump per tile in softmax units (scale 1/sqrt(128), |q . u| ~ 4)
+    gain = (ramp * jump * math.sqrt(128) / 4.0).view(1, L, 1, 1)
+    k = (torch.randn(B, L, H, 128, generator=g) * 0.3 + gain * u).to(torch.bfloat16)
+    v = (torch.randn(B, L, H, 128, generator=g) * 0.5).to(torch.bfloat16)
+    ref = O.attention_ref(q, k, v)
+    for splits in (1, 3):
+        out = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV))], num_splits=splits)
+        assert_parity(out, ref, f"jump {jump} splits {splits}")
+    po, pm, pl = attention_partial(q.to(DEV), [(k.to(DEV), v.to(DEV))])
+    _, (ro, rm, rl) = O.attention_ref(q, k, v, return_partials=True)
+    assert torch.allclose(pm.cpu(), rm, rtol=1e-4, atol=1e-3)  # fp32 sums of ~1e4-sized scores
+
+
 def test_partials_match_oracle_and_merge(lib):
     from lbw_amd import attention_merge, attention_partial
     q, ks, vs = _case(1, 150, 2, [500, 260], seed=21)
