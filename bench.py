@@ -124,12 +124,36 @@ def cpu_baseline(budget_s: float = 12.0):
                       f"ms per 40-layer chunk extrapolated: {dt / heads * H * 40 * 1e3:.0f}"}
 
 
-def _time_ms(fn, iters=10, warmup=2):
+_SLEEP_CYCLES_PER_MS = []
+
+
+def _gpu_busy(ms: float):
+    """Queue about ``ms`` of GPU spinning (torch.cuda._sleep, a bounded clock loop) on the
+    current stream, calibrated once with events."""
     import torch
-    for _ in range(warmup):
+    if not _SLEEP_CYCLES_PER_MS:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        torch.cuda._sleep(1_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS.append(1_000_000 / max(e0.elapsed_time(e1), 1e-3))
+    torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS[0] * ms))
+
+
+def _time_ms(fn, iters=10, warmup=2):
+    """GPU time per call of ``fn``. The GPU is kept busy while the host queues the timed calls,
+    so that the Python/ctypes time between launches of a short kernel is not counted."""
+    import torch
+    host_ms = 1.0
+    for _ in range(max(warmup, 2)):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
         fn()
+        host_ms = (time.perf_counter() - t0) * 1e3   # host time of one launch (the last one)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _gpu_busy(min(2.0 + 2.0 * host_ms * iters, 500.0))
     e0.record()
     for _ in range(iters):
         fn()
@@ -183,6 +207,26 @@ def other_configs(dev):
         "ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
         "pct_fp8_peak": round(fl / ms / 1e9 / PEAK_FP8_TFLOPS * 100, 2),
         "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2)}
+    del q, k8, v8
+    # fused q/k norm + RoPE with head-major d-major outputs [H, D, L] (q scaled by 1/sqrt(D)),
+    # 14B 720p chunk; four input/output sets in turn so that the MALL does not serve the reads
+    from lbw_amd import causal_rope_tables, qk_norm_rope_, wan_rope_freqs
+    tabs = causal_rope_tables(wan_rope_freqs(D), GRID, START_FRAME, device=dev)
+    w = (1 + 0.1 * torch.randn(C, generator=g, device=dev)).to(torch.bfloat16)
+    sets = [(rnd(LQ, C), rnd(LQ, C), torch.empty(H, D, LQ, dtype=torch.bfloat16, device=dev),
+             torch.empty(H, D, LQ, dtype=torch.bfloat16, device=dev)) for _ in range(4)]
+    turn = [0]
+
+    def qk_t():
+        xq, xk, oq, ok = sets[turn[0] % len(sets)]
+        turn[0] += 1
+        qk_norm_rope_(xq, xk, None, None, w, w, tabs, EPS, H, q_out=oq, k_out=ok,
+                      q_scale=1.0 / math.sqrt(D), layout="dmajor")
+    ms = _time_ms(qk_t, iters=40)
+    by = 2.0 * 4 * LQ * C
+    out["wan14b_720p_qk_norm_rope_t_dmajor"] = {
+        "ms": round(ms, 4), "GB/s": round(by / ms / 1e6, 1),
+        "pct_hbm_peak": round(by / ms / 1e6 / PEAK_HBM_GBS * 100, 2)}
     return out
 
 
@@ -334,8 +378,11 @@ def main():
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(stop)
     ms_step = total_ms / args.steps
-    qk_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
-    attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
+    qk_all = sorted(e[0].elapsed_time(e[1]) for e in evs)
+    attn_all = sorted(e[1].elapsed_time(e[2]) for e in evs)
+    qk_ms = sum(qk_all) / len(qk_all)
+    attn_ms = sum(attn_all) / len(attn_all)
+    pct = lambda xs, f: xs[min(len(xs) - 1, int(f * len(xs)))]
     flops_layer = attn_flops()
     value = flops_layer * len(layers) / (ms_step / 1e3) / 1e12
     achieved = flops_layer / (attn_ms / 1e3) / 1e12
@@ -362,6 +409,8 @@ def main():
         "ms_per_layer": round(ms_step / len(layers), 4),
         "attn_ms_per_layer": round(attn_ms, 4),
         "qk_norm_rope_ms_per_layer": round(qk_ms, 4),
+        "attn_ms_p10_p50_p90": [round(pct(attn_all, f), 4) for f in (0.1, 0.5, 0.9)],
+        "qk_norm_rope_ms_p10_p50_p90": [round(pct(qk_all, f), 4) for f in (0.1, 0.5, 0.9)],
         "pct_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),

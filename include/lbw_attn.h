@@ -115,11 +115,21 @@ int lbw_attn_merge(int32_t n_parts, const float* const* part_o, const float* con
 
 /* Fused q/k post-processing of one chunk (kernels/qk_post.py semantics, full-row RMSNorm):
  *   y = x + b (fp32); r = rsqrt(sum(y^2)/C + eps); t = bf16(y*r) * gamma (fp32);
- *   Wan 3-D RoPE on interleaved pairs (fp32); out = bf16(t_rot * out_scale).
- * Tokens >= f*h*w pass the RoPE unrotated. The RoPE tables are the per-axis cos/sin rows,
- * packed fp32: cos_t[f][s0], sin_t[f][s0], cos_h[h][s1], sin_h[h][s1], cos_w[w][s1],
- * sin_w[w][s1] with s0 + 2*s1 = head_dim/2. Optionally copies v into v_out (the KV-cache
- * commit of the new chunk's V). k_out/v_out may point into a KV cache slot. */
+ *   Wan 3-D RoPE on interleaved pairs in fp32 with the output scale folded into cos and sin
+ *   (kernels/qk_post.py:259-265): out = bf16(re*(cos*s) - im*(sin*s), re*(sin*s) + im*(cos*s)).
+ * Tokens >= f*h*w pass the RoPE unrotated (out = bf16(t*s)). The RoPE tables are the per-axis
+ * cos/sin rows, packed fp32: cos_t[f][s0], sin_t[f][s0], cos_h[h][s1], sin_h[h][s1],
+ * cos_w[w][s1], sin_w[w][s1] with s0 + 2*s1 = head_dim/2. Optionally copies v into v_out (the
+ * KV-cache commit of the new chunk's V; always rows). k_out/v_out may point into a KV cache slot.
+ * out_layout LBW_QK_ROWS: q_out/k_out are bf16 rows [L, C], *_out_stride = row stride.
+ * out_layout LBW_QK_DMAJOR (kernels/qk_post.py:216-306, qk_norm_rope_t): q_out/k_out are
+ * [H, D, L] with token stride 1, *_out_stride = the d stride (>= L; e.g. the capacity of a
+ * [H, D, capacity] cache, with the pointer at the slot's first token) and head stride
+ * D * d stride.
+ * k == NULL processes q alone (kernels/qk_post.py:144-215, 308-402: x_norm_rope,
+ * x_norm_rope_t3); wk and k_out are then ignored. */
+#define LBW_QK_ROWS 0
+#define LBW_QK_DMAJOR 1
 typedef struct lbw_qk_norm_rope_params {
   int32_t tokens, dim, heads;      /* L, C = heads * head_dim */
   const void* q; int64_t q_stride; /* bf16 rows [L, C], row stride in elements */
@@ -134,6 +144,7 @@ typedef struct lbw_qk_norm_rope_params {
   float q_out_scale, k_out_scale;  /* 1.0 = none */
   const void* v; int64_t v_stride; /* optional V copy (bf16 [L, C]); NULL = none */
   void* v_out; int64_t v_out_stride;
+  int32_t out_layout;              /* LBW_QK_ROWS or LBW_QK_DMAJOR */
 } lbw_qk_norm_rope_params;
 
 int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream);

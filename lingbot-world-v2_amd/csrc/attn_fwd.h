@@ -77,9 +77,16 @@ struct QkNormRopeArgs {
   float q_scale, k_scale;
   const uint16_t* v; int64_t vs;
   uint16_t* vo; int64_t vos;
+  int layout;          // QK_LAYOUT_ROWS: qos/kos are row strides; QK_LAYOUT_DMAJOR: d strides
+  int qo_vec, ko_vec;  // d-major: outputs allow 16-byte stores of 8 tokens
 };
+constexpr int QK_LAYOUT_ROWS = 0;
+constexpr int QK_LAYOUT_DMAJOR = 1;
 hipError_t launch_qk_norm_rope(const QkNormRopeArgs& a, hipStream_t stream);
 int qk_norm_rope_max_table_floats();
+size_t qk_norm_rope_lds_bytes(int ntab, int C, int layout);
+size_t qk_norm_rope_lds_limit();
+int qk_norm_rope_dmajor_max_dim();
 
 struct KvQuantArgs {
   const uint16_t* x;

@@ -376,14 +376,39 @@ int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream) {
     return fail(LBW_ERR_UNSUPPORTED, "rope tables of %lld floats exceed %d", (long long)ntab,
                 qk_norm_rope_max_table_floats());
   if (gt > 0 && p->rope == nullptr) return fail(LBW_ERR_INVALID, "rope tables missing");
+  if (p->out_layout != LBW_QK_ROWS && p->out_layout != LBW_QK_DMAJOR)
+    return fail(LBW_ERR_INVALID, "out_layout %d: LBW_QK_ROWS or LBW_QK_DMAJOR", p->out_layout);
+  const bool dmajor = p->out_layout == LBW_QK_DMAJOR;
+  if (dmajor && p->dim > qk_norm_rope_dmajor_max_dim())
+    return fail(LBW_ERR_UNSUPPORTED, "d-major output: dim %d above %d", p->dim,
+                qk_norm_rope_dmajor_max_dim());
+  if (dmajor && qk_norm_rope_lds_bytes((int)ntab, p->dim, QK_LAYOUT_DMAJOR) > qk_norm_rope_lds_limit())
+    return fail(LBW_ERR_UNSUPPORTED, "d-major output: rope tables (%lld floats) and dim %d exceed LDS",
+                (long long)ntab, p->dim);
   if (p->tokens == 0) return LBW_OK;
-  const void* ptrs[] = {p->q, p->k, p->wq, p->wk, p->q_out, p->k_out};
+  const bool has_k = p->k != nullptr;
+  const void* ptrs[] = {p->q, p->wq, has_k ? p->k : p->q, has_k ? p->wk : p->wq};
   for (const void* q : ptrs)
-    if (q == nullptr || !aligned16(q)) return fail(LBW_ERR_INVALID, "q/k/gamma/outputs must be 16-byte aligned");
-  if ((p->bq && !aligned16(p->bq)) || (p->bk && !aligned16(p->bk)))
+    if (q == nullptr || !aligned16(q)) return fail(LBW_ERR_INVALID, "q/k/gamma must be 16-byte aligned");
+  if ((p->bq && !aligned16(p->bq)) || (has_k && p->bk && !aligned16(p->bk)))
     return fail(LBW_ERR_INVALID, "bias must be 16-byte aligned");
-  if (!mult8(p->q_stride) || !mult8(p->k_stride) || !mult8(p->q_out_stride) || !mult8(p->k_out_stride))
-    return fail(LBW_ERR_INVALID, "row strides must be multiples of 8 elements");
+  if (!mult8(p->q_stride) || (has_k && !mult8(p->k_stride)))
+    return fail(LBW_ERR_INVALID, "input row strides must be multiples of 8 elements");
+  if (p->q_out == nullptr || (has_k && p->k_out == nullptr))
+    return fail(LBW_ERR_INVALID, "q_out/k_out missing");
+  if (!dmajor) {
+    if (!aligned16(p->q_out) || (has_k && !aligned16(p->k_out)))
+      return fail(LBW_ERR_INVALID, "row outputs must be 16-byte aligned");
+    if (!mult8(p->q_out_stride) || (has_k && !mult8(p->k_out_stride)))
+      return fail(LBW_ERR_INVALID, "output row strides must be multiples of 8 elements");
+  } else {
+    if ((reinterpret_cast<uintptr_t>(p->q_out) & 1) ||
+        (has_k && (reinterpret_cast<uintptr_t>(p->k_out) & 1)))
+      return fail(LBW_ERR_INVALID, "d-major outputs must be 2-byte aligned");
+    if (p->q_out_stride < p->tokens || (has_k && p->k_out_stride < p->tokens))
+      return fail(LBW_ERR_INVALID, "d-major outputs: d stride %lld/%lld below tokens %d",
+                  (long long)p->q_out_stride, (long long)p->k_out_stride, p->tokens);
+  }
   if (p->v != nullptr && (p->v_out == nullptr || !aligned16(p->v) || !aligned16(p->v_out) ||
                           !mult8(p->v_stride) || !mult8(p->v_out_stride)))
     return fail(LBW_ERR_INVALID, "v copy: aligned v and v_out with 8-element strides needed");
@@ -391,9 +416,11 @@ int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream) {
   memset(&a, 0, sizeof(a));
   a.L = p->tokens; a.C = p->dim; a.H = p->heads;
   a.q = static_cast<const uint16_t*>(p->q); a.qs = p->q_stride;
-  a.k = static_cast<const uint16_t*>(p->k); a.ks = p->k_stride;
-  a.bq = static_cast<const uint16_t*>(p->bq); a.bk = static_cast<const uint16_t*>(p->bk);
-  a.wq = static_cast<const uint16_t*>(p->wq); a.wk = static_cast<const uint16_t*>(p->wk);
+  if (has_k) {
+    a.k = static_cast<const uint16_t*>(p->k); a.ks = p->k_stride;
+    a.bk = static_cast<const uint16_t*>(p->bk); a.wk = static_cast<const uint16_t*>(p->wk);
+  }
+  a.bq = static_cast<const uint16_t*>(p->bq); a.wq = static_cast<const uint16_t*>(p->wq);
   a.eps = p->eps;
   a.inv_c = 1.0f / (float)p->dim;
   a.rope = p->rope;
@@ -401,7 +428,10 @@ int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream) {
   a.ntab = (int)ntab;
   if (gt == 0) { a.gf = 0; a.gh = 1; a.gw = 1; a.ntab = 0; }
   a.qo = static_cast<uint16_t*>(p->q_out); a.qos = p->q_out_stride;
-  a.ko = static_cast<uint16_t*>(p->k_out); a.kos = p->k_out_stride;
+  if (has_k) { a.ko = static_cast<uint16_t*>(p->k_out); a.kos = p->k_out_stride; }
+  a.layout = dmajor ? QK_LAYOUT_DMAJOR : QK_LAYOUT_ROWS;
+  a.qo_vec = aligned16(p->q_out) && mult8(p->q_out_stride);
+  a.ko_vec = has_k && aligned16(p->k_out) && mult8(p->k_out_stride);
   a.q_scale = p->q_out_scale; a.k_scale = p->k_out_scale;
   a.v = static_cast<const uint16_t*>(p->v); a.vs = p->v_stride;
   a.vo = static_cast<uint16_t*>(p->v_out); a.vos = p->v_out_stride;

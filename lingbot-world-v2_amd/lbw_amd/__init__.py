@@ -12,13 +12,15 @@ from .chunked_kv_cache import (FlatKVCache, allocate_self_kv_chunks, allocate_se
                                chunk_routing, num_chunks)
 from .fp8 import Fp8KV, attention_fp8kv, quantize_kv_fp8
 from .layer import WanCrossAttention, WanSelfAttention
-from .qk_post import qk_norm_rope, qk_norm_rope_
+from .qk_post import (qk_norm_rope, qk_norm_rope3, qk_norm_rope_, qk_norm_rope_t, qk_norm_rope_t3,
+                      x_norm_rope, x_norm_rope_t3)
 from .rope import RopeTables, causal_rope_tables, rope_params, wan_rope_freqs
 
 __all__ = [
     "attention", "flash_attention", "exact_attention", "exact_attention_chunks",
     "cross_attention", "padding_start", "attention_partial", "attention_merge", "attention_segments",
-    "qk_norm_rope", "qk_norm_rope_", "RopeTables", "causal_rope_tables", "rope_params",
+    "qk_norm_rope", "qk_norm_rope_", "qk_norm_rope3", "qk_norm_rope_t", "qk_norm_rope_t3",
+    "x_norm_rope", "x_norm_rope_t3", "RopeTables", "causal_rope_tables", "rope_params",
     "wan_rope_freqs", "Fp8KV", "quantize_kv_fp8", "attention_fp8kv", "FlatKVCache",
     "allocate_self_kv_chunks", "allocate_self_kv_chunks_fp8", "chunk_routing", "num_chunks", "WanSelfAttention",
     "WanCrossAttention",

@@ -65,6 +65,7 @@ class QkNormRopeParams(ctypes.Structure):
         ("q_out_scale", ctypes.c_float), ("k_out_scale", ctypes.c_float),
         ("v", ctypes.c_void_p), ("v_stride", ctypes.c_int64),
         ("v_out", ctypes.c_void_p), ("v_out_stride", ctypes.c_int64),
+        ("out_layout", ctypes.c_int32),
     ]
 
 

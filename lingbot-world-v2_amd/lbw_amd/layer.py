@@ -142,9 +142,8 @@ class WanCrossAttention:
         """RMSNorm of projected rows [L, C] (no rotation) through the fused kernel."""
         L = x_raw.shape[0]
         out = torch.empty(L, self.C, dtype=torch.bfloat16, device=x_raw.device)
-        scratch = torch.empty_like(out)
-        qk_norm_rope_(x_raw, x_raw, bias, bias, gamma, gamma, _no_rope(x_raw.device, self.head_dim),
-                      self.eps, self.heads, q_out=out, k_out=scratch)
+        qk_norm_rope_(x_raw, None, bias, None, gamma, None, _no_rope(x_raw.device, self.head_dim),
+                      self.eps, self.heads, q_out=out, k_out=None)
         return out
 
     def set_context(self, context):

@@ -6,7 +6,8 @@ reference's own PyTorch semantics of the hot path:
   * Wan RoPE tables and the causal 3-D grid (wan/modules/model.py:47-53, 480-487;
     wan/modules/model_fast.py:878-979)
   * RMSNorm of q/k, both as the nn.Module (model.py:126-142) and as the fused
-    q/k post-processing kernel sequence (kernels/qk_post.py:88-141)
+    q/k post-processing kernel sequence (kernels/qk_post.py:88-141), token rows and the
+    head-major d-major ``_t`` layout with q's scale folded into cos/sin (qk_post.py:216-306)
   * windowed exact attention, the SDPA fallback of attention() (attention.py:1127-1143)
     with the KV window mask of model_fast.py:2538-2545, looped per head and query
     block so no [H, Lq, Lk] score tensor is ever materialised

@@ -13,7 +13,7 @@ import torch
 __all__ = [
     "MAX_LATENT_FRAMES", "rope_params", "wan_rope_freqs", "rope_axis_split",
     "causal_rope_grids", "rope_axis_tables", "expand_axis_tables", "rope_apply_rotation",
-    "rms_norm_module", "qk_post_norm_rope", "qk_post_ss", "attention_ref", "sdpa_ref",
+    "rms_norm_module", "qk_post_norm_rope", "qk_post_norm_rope_t", "qk_post_ss", "attention_ref", "sdpa_ref",
     "attention_brute_f64", "merge_partials", "window_mask", "num_chunks", "chunk_routing",
     "ordered_chunks", "flat_cache_write_plan", "fp8_e4m3_encode", "fp8_e4m3_decode",
     "quantize_kv_fp8", "dequantize_kv_fp8", "self_attention_layer_ref", "cross_kv_ref",
@@ -133,11 +133,12 @@ def qk_post_norm_rope(x: torch.Tensor, bias: torch.Tensor | None, weight: torch.
         y  = x + b                                   (fp32)
         r  = rsqrt(sum(y^2) / C + eps)               (fp32, full-row sum)
         t  = bf16(y * r) * w                         (one bf16 rounding, x gamma in fp32)
-        RoPE on interleaved pairs with cos/sin [L', D/2] fp32; rows >= L' pass through
-        out = bf16(rope(t) * out_scale)
+        RoPE on interleaved pairs with cos/sin [L', D/2] fp32, the output scale s folded
+        into them first (fp32 cos*s, sin*s); rows >= L' are t*s
+        out = bf16(that)
 
-    ``out_scale`` restates the ``_t`` variants' 1/sqrt(D) pre-scale of q (qk_post.py:259-265).
-    Returns bf16 ``[L, C]``."""
+    ``out_scale`` restates the ``_t`` variants' pre-scale of q by 1/sqrt(D), which rides on
+    q's cos/sin (qk_post.py:259-265, 359-365). Returns bf16 ``[L, C]``."""
     L, C = x.shape
     y = x.float() + (bias.float() if bias is not None else 0.0)
     ss = (y * y).sum(-1)
@@ -145,8 +146,26 @@ def qk_post_norm_rope(x: torch.Tensor, bias: torch.Tensor | None, weight: torch.
     t = (y * r[:, None]).to(torch.bfloat16).float() * weight.float().view(1, C)
     D = 2 * cos.shape[1]
     H = heads if heads is not None else C // D
-    out = rope_apply_rotation(t.view(L, H, D), cos.float(), sin.float(), torch.float32)
-    return (out.reshape(L, C) * out_scale).to(torch.bfloat16)
+    S = cos.shape[0]
+    s = torch.tensor(out_scale, dtype=torch.float32)
+    out = rope_apply_rotation(t.view(L, H, D), cos.float() * s, sin.float() * s, torch.float32)
+    out = out.reshape(L, C)
+    if out_scale != 1.0:
+        out = torch.cat([out[:S], out[S:] * s])
+    return out.to(torch.bfloat16)
+
+
+def qk_post_norm_rope_t(x: torch.Tensor, bias: torch.Tensor | None, weight: torch.Tensor,
+                        cos: torch.Tensor, sin: torch.Tensor, eps: float = 1e-6,
+                        heads: int | None = None, out_scale: float = 1.0) -> torch.Tensor:
+    """kernels/qk_post.py:228-306 (``_qk_norm_rope_t_body``) and 331-402 (``_x_norm_rope_t3``):
+    the same values as :func:`qk_post_norm_rope` written head-major, d-major: bf16
+    ``[H, D, L]`` with element ``(h, d, l)`` = row ``l``'s feature ``h * D + d``."""
+    L, C = x.shape
+    D = 2 * cos.shape[1]
+    H = heads if heads is not None else C // D
+    rows = qk_post_norm_rope(x, bias, weight, cos, sin, eps, H, out_scale)
+    return rows.view(L, H, D).permute(1, 2, 0).contiguous()
 
 
 # ----------------------------------------------------------------------------- attention

@@ -80,6 +80,31 @@ def test_entry_points_reject_bad_arguments_without_gpu():
     assert lib.lbw_kv_quant_fp8(None, 1, 10, 1, 128, 0, 0, 0, None, None, 32, None) == 2
 
 
+def test_qk_norm_rope_layout_checks_without_gpu():
+    """out_layout validation (rows / d-major) runs before any HIP call."""
+    from lbw_amd import _lib
+    lib = ctypes.CDLL(_lib_path())
+    _lib._declare(lib)
+    fake = 1 << 20                                   # aligned, never dereferenced
+    p = _lib.QkNormRopeParams()
+    p.tokens, p.dim, p.heads, p.s0, p.s1 = 16, 512, 4, 22, 21
+    p.q = p.wq = p.q_out = fake
+    p.q_stride = 512
+    p.out_layout = 7
+    assert lib.lbw_qk_norm_rope(ctypes.byref(p), None) == 1
+    assert b"out_layout" in lib.lbw_last_error()
+    p.out_layout = 1                                 # d-major: the d stride must cover the tokens
+    p.q_out_stride = 8
+    assert lib.lbw_qk_norm_rope(ctypes.byref(p), None) == 1
+    assert b"d stride" in lib.lbw_last_error()
+    p.dim, p.heads = 6144, 48                        # two rows of more than 5120 features
+    assert lib.lbw_qk_norm_rope(ctypes.byref(p), None) == 2
+    assert b"d-major" in lib.lbw_last_error()
+    p.dim, p.heads, p.out_layout, p.q_out_stride = 512, 4, 0, 512
+    p.q_out = fake + 2                               # rows layout needs 16-byte aligned outputs
+    assert lib.lbw_qk_norm_rope(ctypes.byref(p), None) == 1
+
+
 def _split_count(H, LQ, LK):
     """KV splits the library plans for q [1, LQ, H, 128] over one LK-key segment, read back
     from the workspace size (splits x rows x (D + 2) fp32; 0 for a single pass). Host-only."""

@@ -146,6 +146,56 @@ def test_qk_post_matches_module_sequence_within_one_rounding():
     assert (fused - mod.float()).abs().mean() < 2e-3
 
 
+def _qk_post_t_inputs(L=2176, F=1280, SEQ=2160, seed=0):
+    """perf/qk_post_t_test.py:18-29's inputs: q, k x1.5, bias x0.2, gamma 1 + 0.1 N, random
+    angles for the first SEQ rows and identity rows after them."""
+    g = torch.Generator().manual_seed(seed)
+    C = 64
+    q = (torch.randn(L, F, generator=g) * 1.5).to(torch.bfloat16)
+    k = (torch.randn(L, F, generator=g) * 1.5).to(torch.bfloat16)
+    bq = (torch.randn(F, generator=g) * 0.2).to(torch.bfloat16)
+    bk = (torch.randn(F, generator=g) * 0.2).to(torch.bfloat16)
+    wq = (1 + torch.randn(F, generator=g) * 0.1).to(torch.bfloat16)
+    wk = (1 + torch.randn(F, generator=g) * 0.1).to(torch.bfloat16)
+    ang = torch.rand(SEQ, C, generator=g) * 6.28
+    return q, k, bq, bk, wq, wk, ang.cos(), ang.sin()
+
+
+def test_qk_post_t_scale_rides_on_cos_sin():
+    """The _t variants' q scale (qk_post.py:259-265): exact for a power of two (scaling
+    commutes with every rounding), and against the reference test's own fp32 formula
+    (perf/qk_post_t_test.py:32-41: rotate, then x 1/sqrt(D)) within bf16 rounding."""
+    q, k, bq, bk, wq, wk, cos, sin = _qk_post_t_inputs()
+    L, F = q.shape
+    one = O.qk_post_norm_rope(q, bq, wq, cos, sin)
+    quarter = O.qk_post_norm_rope(q, bq, wq, cos, sin, out_scale=0.25)
+    assert torch.equal(quarter, (one.float() * 0.25).to(torch.bfloat16))
+    qs = 1.0 / math.sqrt(128)
+    got = O.qk_post_norm_rope(q, bq, wq, cos, sin, out_scale=qs).float()
+    y = q.float() + bq.float()
+    r = torch.rsqrt((y * y).sum(-1) / F + 1e-6)
+    t = (y * r[:, None]).to(torch.bfloat16).float() * wq.float()
+    t4 = t.view(L, F // 128, 64, 2)
+    cb = torch.cat([cos, torch.ones(L - cos.shape[0], 64)])[:, None, :]
+    sb = torch.cat([sin, torch.zeros(L - sin.shape[0], 64)])[:, None, :]
+    want = torch.stack([t4[..., 0] * cb - t4[..., 1] * sb, t4[..., 0] * sb + t4[..., 1] * cb],
+                       -1).reshape(L, F) * qs
+    assert ((got - want).norm() / want.norm()).item() < 3e-3
+    assert ((got - want).abs() <= want.abs() * 2.0 ** -7 + 1e-3).float().mean() > 0.999
+    # rows past the grid are scaled only
+    assert torch.allclose(got[2160:], (t[2160:] * qs).to(torch.bfloat16).float())
+
+
+def test_qk_post_t_layout_is_head_major_d_major():
+    q, k, bq, bk, wq, wk, cos, sin = _qk_post_t_inputs(L=40, F=384, SEQ=33)
+    rows = O.qk_post_norm_rope(k, bk, wk, cos, sin)
+    t = O.qk_post_norm_rope_t(k, bk, wk, cos, sin)
+    assert t.shape == (3, 128, 40)
+    for h, d, l in [(0, 0, 0), (1, 5, 7), (2, 127, 39), (2, 3, 35)]:
+        assert t[h, d, l] == rows[l, 128 * h + d]
+    assert torch.equal(t.permute(2, 0, 1).reshape(40, 384), rows)
+
+
 # ----------------------------------------------------------------------------- attention
 def _qkv(B, Lq, Lk, H, D, seed=0, gain=1.0):
     g = torch.Generator().manual_seed(seed)
