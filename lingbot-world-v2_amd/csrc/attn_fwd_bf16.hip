@@ -492,7 +492,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
       // schedule: the first pairs' fragments, then per MFMA pair: MFMA, 4 VALU, MFMA, 4 VALU,
       // the LDS reads of the pairs K_AHEAD / V_AHEAD ahead (the VALU work spread over the
-      // whole step measured faster than larger groups that finish it early)
+      // whole step measured faster than larger groups that finish it early). This shapes the
+      // TRACK step only: without TRACK these groups fall after the redo branch, in a block
+      // with no MFMAs, and the compiler's own order of the step (measured 2 % faster than
+      // this pattern placed ahead of the branch) stands.
       constexpr int NDS0 = (KPRE ? 0 : K_AHEAD) + (VPRE ? 0 : 2 * V_AHEAD);
       if constexpr (NDS0 > 0) __builtin_amdgcn_sched_group_barrier(0x100, NDS0, 0);
 #pragma unroll
