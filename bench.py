@@ -227,6 +227,31 @@ def other_configs(dev):
     out["wan14b_720p_qk_norm_rope_t_dmajor"] = {
         "ms": round(ms, 4), "GB/s": round(by / ms / 1e6, 1),
         "pct_hbm_peak": round(by / ms / 1e6 / PEAK_HBM_GBS * 100, 2)}
+    del sets
+    # the whole self-attention of one 14B block at the 720p chunk: fused QKV GEMM (hipBLASLt,
+    # V bias in its epilogue) -> fused q/k norm + RoPE + KV commit -> attention over the
+    # 46800-token flat cache -> o-projection GEMM; random-init weights N(0, 0.02)
+    from lbw_amd import FlatKVCache, WanSelfAttention
+    wts = [(0.02 * torch.randn(C, C, generator=g, device=dev)).to(torch.bfloat16) for _ in range(4)]
+    vec = lambda sc, off: (off + sc * torch.randn(C, generator=g, device=dev)).to(torch.bfloat16)
+    layer = WanSelfAttention(wts[0], vec(0.02, 0), wts[1], vec(0.02, 0), wts[2], vec(0.02, 0),
+                             wts[3], vec(0.02, 0), vec(0.1, 1.0), vec(0.1, 1.0), heads=H)
+    cache = FlatKVCache(1, LK, H, D, device=dev, local_attn_size=-1)
+    cache.k.copy_(rnd(1, LK, H, D))
+    cache.v.copy_(rnd(1, LK, H, D))
+    x = rnd(1, LQ, C)
+    start = LK - LQ
+
+    def layer_fwd():
+        cache.global_end = cache.local_end = start
+        layer.forward(x, GRID, START_FRAME, cache, start)
+    ms = _time_ms(layer_fwd, iters=10)
+    fl_proj = 4 * 2.0 * LQ * C * C
+    fl = attn_flops() + fl_proj
+    out["wan14b_720p_selfattn_layer_with_projections"] = {
+        "ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
+        "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2),
+        "projection_TFLOP": round(fl_proj / 1e12, 4)}
     return out
 
 

@@ -44,6 +44,9 @@ class WanSelfAttention:
         self.head_dim = self.C // heads
         self.eps = eps
         self.w_qkv = torch.cat([wq, wk, wv], 0).contiguous()         # [3C, C]
+        # the GEMM epilogue adds V's bias (one rounding, as nn.Linear); q's and k's biases are
+        # added in fp32 by the fused norm kernel (kernels/qk_post.py), so theirs are zero here
+        self.b_qkv = None if bv is None else torch.cat([torch.zeros_like(bv), torch.zeros_like(bv), bv])
         self.bq, self.bk, self.bv = bq, bk, bv
         self.wo, self.bo = wo, bo
         self.gq, self.gk = gq, gk
@@ -52,14 +55,13 @@ class WanSelfAttention:
     def _project_norm_rope(self, x, grid, start_frame, k_out, v_out):
         """x [1, L, C] -> q' [L, C] (bf16) and K/V written into k_out / v_out ([L, C] views)."""
         L = x.shape[1]
-        qkv = F.linear(x[0], self.w_qkv)                                # [L, 3C] bf16, no bias
+        qkv = F.linear(x[0], self.w_qkv, self.b_qkv)                    # [L, 3C] bf16
         C = self.C
-        q_raw, k_raw, v_raw = qkv[:, :C], qkv[:, C:2 * C], qkv[:, 2 * C:]
-        v = v_raw + self.bv if self.bv is not None else v_raw
+        q_raw, k_raw, v = qkv[:, :C], qkv[:, C:2 * C], qkv[:, 2 * C:]   # row-strided views
         tabs = causal_rope_tables(self.freqs, grid, start_frame, device=x.device)
         q = torch.empty(L, C, dtype=torch.bfloat16, device=x.device)
         qk_norm_rope_(q_raw, k_raw, self.bq, self.bk, self.gq, self.gk, tabs, self.eps,
-                      self.heads, q_out=q, k_out=k_out, v=v.contiguous(), v_out=v_out)
+                      self.heads, q_out=q, k_out=k_out, v=v, v_out=v_out)
         return q
 
     def prefill(self, x, grid, start_frame, cache: FlatKVCache, current_start: int = 0):
