@@ -5,12 +5,15 @@
 // written as bf16; a row whose every split is empty (all m_s = -inf) yields 0.
 //
 // HBM-bound: per (b, h, q) row it reads n * (D + 2) fp32 values and writes D bf16 values.
-// One thread per (row, 4 consecutive d), so every load and store is a 16 / 8-byte vector.
+// One thread per (row, 4 consecutive d), so every load and store is a 16 / 8-byte vector. The
+// split count is a template parameter, so that a thread issues all of its 3 n loads before it
+// waits for any of them (with a runtime count the loops kept one round trip per load in flight).
 
 #include "attn_tiles.h"
 
 namespace lbw {
 
+template <int N>
 __global__ void __launch_bounds__(256)
 attn_merge_kernel(const MergeKernelArgs a) {
   const int64_t total = (int64_t)a.B * a.H * a.Lq * (a.D / 4);
@@ -22,17 +25,25 @@ attn_merge_kernel(const MergeKernelArgs a) {
     const int64_t bh = row / a.Lq;
     const int h = (int)(bh % a.H);
     const int b = (int)(bh / a.H);
+    float ms[N], ls[N];
+    floatx4 os[N];
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+      ms[s] = a.m[s][row];
+      ls[s] = a.l[s][row];
+      os[s] = *reinterpret_cast<const floatx4*>(a.o[s] + row * a.D + 4 * dq);
+    }
     float M = -INFINITY;
-    for (int s = 0; s < a.n; ++s) M = fmaxf(M, a.m[s][row]);
+#pragma unroll
+    for (int s = 0; s < N; ++s) M = fmaxf(M, ms[s]);
     float den = 0.0f;
     floatx4 num = {0.f, 0.f, 0.f, 0.f};
     if (M != -INFINITY) {
-      for (int s = 0; s < a.n; ++s) {
-        const float ms = a.m[s][row];
-        const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);
-        den += w * a.l[s][row];
-        const floatx4 o = *reinterpret_cast<const floatx4*>(a.o[s] + row * a.D + 4 * dq);
-        num += w * o;
+#pragma unroll
+      for (int s = 0; s < N; ++s) {
+        const float w = (ms[s] == -INFINITY) ? 0.0f : expf(ms[s] - M);
+        den += w * ls[s];
+        num += w * os[s];
       }
     }
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
@@ -53,7 +64,26 @@ hipError_t launch_attn_merge(const MergeKernelArgs& a, hipStream_t stream) {
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((uint32_t)blocks), dim3(256), 0, stream, a);
+  const dim3 grid((uint32_t)blocks), block(256);
+  switch (a.n) {
+    case 1: hipLaunchKernelGGL(attn_merge_kernel<1>, grid, block, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL(attn_merge_kernel<2>, grid, block, 0, stream, a); break;
+    case 3: hipLaunchKernelGGL(attn_merge_kernel<3>, grid, block, 0, stream, a); break;
+    case 4: hipLaunchKernelGGL(attn_merge_kernel<4>, grid, block, 0, stream, a); break;
+    case 5: hipLaunchKernelGGL(attn_merge_kernel<5>, grid, block, 0, stream, a); break;
+    case 6: hipLaunchKernelGGL(attn_merge_kernel<6>, grid, block, 0, stream, a); break;
+    case 7: hipLaunchKernelGGL(attn_merge_kernel<7>, grid, block, 0, stream, a); break;
+    case 8: hipLaunchKernelGGL(attn_merge_kernel<8>, grid, block, 0, stream, a); break;
+    case 9: hipLaunchKernelGGL(attn_merge_kernel<9>, grid, block, 0, stream, a); break;
+    case 10: hipLaunchKernelGGL(attn_merge_kernel<10>, grid, block, 0, stream, a); break;
+    case 11: hipLaunchKernelGGL(attn_merge_kernel<11>, grid, block, 0, stream, a); break;
+    case 12: hipLaunchKernelGGL(attn_merge_kernel<12>, grid, block, 0, stream, a); break;
+    case 13: hipLaunchKernelGGL(attn_merge_kernel<13>, grid, block, 0, stream, a); break;
+    case 14: hipLaunchKernelGGL(attn_merge_kernel<14>, grid, block, 0, stream, a); break;
+    case 15: hipLaunchKernelGGL(attn_merge_kernel<15>, grid, block, 0, stream, a); break;
+    case 16: hipLaunchKernelGGL(attn_merge_kernel<16>, grid, block, 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
