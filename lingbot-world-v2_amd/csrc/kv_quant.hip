@@ -6,6 +6,7 @@
 //   code  = round_to_nearest_even_e4m3fn(x * inv)
 // One workgroup per (b, h, block): the block's 64 x 128 bf16 values are read once into
 // registers (16-byte loads, 16 lanes per token row), reduced to amax, encoded and written.
+// Workgroups are numbered with (b, h) fastest.
 
 #include "common.h"
 #include "attn_fwd.h"
@@ -33,8 +34,11 @@ __device__ __forceinline__ uint32_t e4m3fn_encode(float x) {
 __global__ void __launch_bounds__(256)
 kv_quant_fp8_kernel(const KvQuantArgs a) {
   __shared__ float red[4];
-  const int64_t blk = blockIdx.x % a.nblk;
-  const int64_t bh = blockIdx.x / a.nblk;
+  // heads fastest: neighbouring workgroups read and write the same token rows (each row holds
+  // every head), which keeps the HBM accesses of concurrent workgroups together
+  const int64_t nbh = (int64_t)a.B * a.H;
+  const int64_t bh = blockIdx.x % nbh;
+  const int64_t blk = blockIdx.x / nbh;
   const int h = (int)(bh % a.H);
   const int b = (int)(bh / a.H);
   const int t = threadIdx.x;
