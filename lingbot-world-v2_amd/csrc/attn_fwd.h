@@ -26,6 +26,7 @@ struct AttnKernelArgs {
   int64_t qsb, qsl, qsh;
   uint16_t* out;
   int64_t osb, osl, osh;
+  int o16;            // out and its strides allow 16-byte stores
   int nseg;
   SegDesc seg[LBW_MAX_SEGS];
   int64_t total;      // keys in the concatenation

@@ -190,9 +190,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       if (q < a.Lq) v = *reinterpret_cast<const u32x4*>(qp + 16 * s);
       qf[s] = v;
     }
-    // Wait for Q here, on every path: otherwise the compiler, which cannot see the asm K/V
-    // copies, re-waits for all memory before the first MFMA of every loop iteration.
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // (waited for below, together with the first K/V tiles: one round trip, not two)
   }
 
   // ---- per-lane LDS offsets
@@ -340,7 +338,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       unsigned char* zv = lds + V_BASE + (NSTAGE - 1) * TILE_B + HALF_B;
       *reinterpret_cast<u32x4*>(zv + 16 * threadIdx.x) = z;
     }
-    if constexpr (!FP8) wait_tiles_outstanding(min(NSTAGE - 2, T - 1));
+    // Q and the first tiles (issued after Q, so the in-order count covers both): wait for all
+    // of them, explicitly and on every path, so that the compiler, which cannot see the asm
+    // K/V copies, does not re-wait for all memory before the first MFMA of every iteration
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero fill (and fp8 tiles) are done
     barrier_nofence();
 
@@ -582,25 +583,45 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     }
   }
 
+  // Every wave is past its last LDS reads (the drain) before the LDS is reused for staging O.
+  barrier_nofence();
   if (!wave_active) return;
 
   // ---- epilogue
-  const int q = q0 + l32;
+  // (a workgroup with no tiles still has its Q loads outstanding)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   const float l_tot = wave_sum_xor32(lsum);
+  // O leaves through this wave's 8 KB of LDS, 32 rows of 256 B with 16-byte chunk c of row r
+  // at physical chunk c ^ (r & 15), and is written back as whole rows, 16 lanes per 256-byte
+  // row segment: 4x fewer cache lines per store than storing the MFMA layout directly (lane
+  // (l32, hl) holds d = 32db + 8g + 4hl .. +3 of row l32).
+  unsigned char* stg = lds + 8192 * wave;
+  const int rrow = lane >> 4, rch = lane & 15;  // read side: row in a 4-row group, chunk
   if (a.mode == kModeNormalized) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (q < a.Lq) {
-      uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)q + a.osh * h;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d0 = 32 * db + 8 * g + 4 * hl;
-          u32x2 w;
-          w[0] = pack_bf16x2(oacc[db][4 * g + 0] * inv, oacc[db][4 * g + 1] * inv);
-          w[1] = pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
-          *reinterpret_cast<u32x2*>(op + d0) = w;
+      for (int g = 0; g < 4; ++g) {
+        u32x2 w;
+        w[0] = pack_bf16x2(oacc[db][4 * g + 0] * inv, oacc[db][4 * g + 1] * inv);
+        w[1] = pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv);
+        *reinterpret_cast<u32x2*>(stg + l32 * 256 + (((4 * db + g) ^ (l32 & 15)) << 4) + 8 * hl) = w;
+      }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int r = 4 * k + rrow;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * 256 + ((rch ^ (r & 15)) << 4));
+      const int qq = q0 + r;
+      if (qq < a.Lq) {
+        uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)qq + a.osh * h + 8 * rch;
+        if (a.o16) {
+          *reinterpret_cast<u32x4*>(op) = v;
+        } else {
+          *reinterpret_cast<u32x2*>(op) = u32x2{v[0], v[1]};
+          *reinterpret_cast<u32x2*>(op + 4) = u32x2{v[2], v[3]};
         }
+      }
     }
   } else {
     // cte_partial contract (TRACK): O and l relative to the true row max, m in scaled units;
@@ -615,24 +636,35 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         m_out = m_used * a.scale;
       }
     }
-    if (q < a.Lq) {
-      const int64_t row = ((int64_t)(split * a.B + b) * a.H + h) * a.Lq + q;
-      float* po = a.part_o + row * D;
+    const int64_t row0 = ((int64_t)(split * a.B + b) * a.H + h) * a.Lq;
+    const int q = q0 + l32;
+    if (q < a.Lq && hl == 0) {
+      a.part_m[row0 + q] = m_out;
+      a.part_l[row0 + q] = l_tot * f;
+    }
+    // fp32 O in two halves of 64 d (256 B per row each)
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int dbh = 0; dbh < 2; ++dbh)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const int d0 = 32 * db + 8 * g + 4 * hl;
+          const int db = 2 * half + dbh;
           floatx4 w;
           w[0] = oacc[db][4 * g + 0] * f;
           w[1] = oacc[db][4 * g + 1] * f;
           w[2] = oacc[db][4 * g + 2] * f;
           w[3] = oacc[db][4 * g + 3] * f;
-          *reinterpret_cast<floatx4*>(po + d0) = w;
+          const int cc = 8 * dbh + 2 * g + hl;  // 16-byte chunk of the half-row
+          *reinterpret_cast<floatx4*>(stg + l32 * 256 + ((cc ^ (l32 & 15)) << 4)) = w;
         }
-      if (hl == 0) {
-        a.part_m[row] = m_out;
-        a.part_l[row] = l_tot * f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int r = 4 * k + rrow;
+        const floatx4 v = *reinterpret_cast<const floatx4*>(stg + r * 256 + ((rch ^ (r & 15)) << 4));
+        const int qq = q0 + r;
+        if (qq < a.Lq)
+          *reinterpret_cast<floatx4*>(a.part_o + (row0 + qq) * D + 64 * half + 4 * rch) = v;
       }
     }
   }

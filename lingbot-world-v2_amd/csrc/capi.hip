@@ -152,6 +152,7 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   a.qsb = p->q_stride_b; a.qsl = p->q_stride_l; a.qsh = p->q_stride_h;
   a.out = static_cast<uint16_t*>(p->out);
   a.osb = p->o_stride_b; a.osl = p->o_stride_l; a.osh = p->o_stride_h;
+  a.o16 = aligned16(p->out) && mult8(p->o_stride_b) && mult8(p->o_stride_l) && mult8(p->o_stride_h);
   a.nseg = p->n_segments;
   int64_t start = 0;
   for (int i = 0; i < p->n_segments; ++i) {
