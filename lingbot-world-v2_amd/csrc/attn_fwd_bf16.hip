@@ -164,18 +164,6 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   const int h = rest % a.H;
   const int b = rest / a.H;
 
-  // ---- key range of this batch and split
-  int64_t hi = a.hi;
-  if (a.k_lens != nullptr) {
-    const int64_t kl = a.k_lens[b];
-    hi = kl < hi ? kl : hi;
-  }
-  const int64_t lo = a.lo;
-  const int n_tiles = hi > lo ? count_tiles(a, lo, hi) : 0;
-  const int per_split = (n_tiles + a.splits - 1) / a.splits;
-  const int t0 = split * per_split;
-  const int t1 = min(n_tiles, t0 + per_split);
-
   const int q0 = qt * BM + wave * 32;  // first query of this wave (wave-uniform)
   const bool wave_active = q0 < a.Lq;
 
@@ -192,6 +180,18 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     }
     // (waited for below, together with the first K/V tiles: one round trip, not two)
   }
+
+  // ---- key range of this batch and split
+  int64_t hi = a.hi;
+  if (a.k_lens != nullptr) {
+    const int64_t kl = a.k_lens[b];
+    hi = kl < hi ? kl : hi;
+  }
+  const int64_t lo = a.lo;
+  const int n_tiles = hi > lo ? count_tiles(a, lo, hi) : 0;
+  const int per_split = (n_tiles + a.splits - 1) / a.splits;
+  const int t0 = split * per_split;
+  const int t1 = min(n_tiles, t0 + per_split);
 
   // ---- per-lane LDS offsets
   // DMA: this wave fills 1 KB blocks NDMA*wave + i of each tile; lane -> (row, physical chunk).

@@ -29,6 +29,10 @@ __device__ __forceinline__ int seg_tiles(const SegDesc& s, int64_t lo, int64_t h
 }
 
 __device__ __forceinline__ int count_tiles(const AttnKernelArgs& a, int64_t lo, int64_t hi) {
+  if (a.nseg == 1) {  // the common call: a constant index lets the descriptor loads batch early
+    int64_t la = 0, lb = 0;
+    return seg_tiles(a.seg[0], lo, hi, la, lb);
+  }
   int n = 0;
 #pragma unroll 1
   for (int i = 0; i < a.nseg; ++i) {
@@ -106,6 +110,12 @@ __device__ __forceinline__ void cursor_init(const AttnKernelArgs& a, int64_t lo,
                                             int g, int b, int h, TileCursor& c) {
   int cum = 0;
   c.seg = a.nseg;
+  if (a.nseg == 1) {
+    int64_t la = 0, lb = 0;
+    const int n = seg_tiles(a.seg[0], lo, hi, la, lb);
+    if (g < n) cursor_enter<ESZ>(a, 0, la, lb, b, h, (int)(la / BN) + g, c);
+    return;
+  }
 #pragma unroll 1
   for (int i = 0; i < a.nseg; ++i) {
     int64_t la = 0, lb = 0;
