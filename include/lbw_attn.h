@@ -82,7 +82,10 @@ typedef struct lbw_attn_params {
   float* part_l;
 } lbw_attn_params;
 
-/* Bytes of workspace lbw_attention_fwd needs for these params (0 when single pass). */
+/* Bytes of workspace lbw_attention_fwd needs for these params: the split-KV partials (when
+ * the call is split) and 256 bytes of work-queue counters, which let the XCDs of the GPU share
+ * out the workgroups by speed. A call given no (or too small a) workspace for an unsplit plan
+ * still runs, with a static workgroup-to-XCD assignment. */
 size_t lbw_attention_workspace_size(const lbw_attn_params* p);
 
 /* Chunk self-attention: softmax(scale * Q K^T) V over the windowed concatenation of the KV

@@ -36,6 +36,7 @@ struct AttnKernelArgs {
   float scale_log2;   // scale * log2(e)
   int B, H, Lq;
   int n_qtiles, splits;
+  uint32_t* queue;    // 8 work-queue counters (zeroed before the launch), or null: static order
   int mode;
   float* part_o;
   float* part_m;

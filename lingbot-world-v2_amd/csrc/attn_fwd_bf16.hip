@@ -140,6 +140,38 @@ __device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
     for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
 }
 
+// Work items. A unit is (batch, head, q-tile); each unit's keys are cut into `splits` equal
+// pieces. XCD x owns the units [U x / 8, U (x + 1) / 8) and runs their pieces piece-major (the
+// q-tiles of a head, which read the same keys, run side by side on one XCD and share its L2).
+// Item j of XCD x is piece j / n_x of unit start_x + j % n_x; the id is piece * U + unit.
+// The XCDs of one GPU do not run equally fast (measured: the odd-numbered ones take 3-5 %
+// longer per item), so with a work queue a workgroup whose own XCD's share is gone takes the
+// next item of another XCD's share.
+__device__ __forceinline__ void xcd_units(uint32_t U, uint32_t x, uint32_t& start, uint32_t& n) {
+  start = (U * x) / 8u;
+  n = (U * (x + 1u)) / 8u - start;
+}
+
+// Next item for a workgroup on XCD x0 from the 8 per-XCD queues, its own XCD's first, then any
+// other (so that faster XCDs take over the end of slower ones' shares); -1 when all are empty.
+// A relaxed read skips exhausted queues without bumping their counters.
+__device__ __forceinline__ int take_item(uint32_t* q, uint32_t U, uint32_t S, uint32_t x0) {
+  for (uint32_t t = 0; t < 8u; ++t) {
+    const uint32_t x = (x0 + t) & 7u;
+    uint32_t st, n;
+    xcd_units(U, x, st, n);
+    const uint32_t size = S * n;
+    if (__hip_atomic_load(&q[x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= size) continue;
+    const uint32_t k = __hip_atomic_fetch_add(&q[x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k < size) return (int)((k / n) * U + st + k % n);
+  }
+  return -1;
+}
+
+__global__ void __launch_bounds__(64) attn_queue_reset_kernel(uint32_t* q) {
+  if (threadIdx.x < 8) q[threadIdx.x] = 0u;
+}
+
 // FP8 = false: bf16 K/V, DMA'd straight into LDS. FP8 = true: e4m3 K/V codes with fp32 scales
 // per (batch, head, 64-token block): each tile is loaded into registers one tile ahead,
 // converted exactly to bf16 (every e4m3 value is a bf16 value) and written into the same LDS
@@ -155,14 +187,31 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   const int hl = lane >> 5;  // k-group / row-half of this lane
   const int l32 = lane & 31;
 
-  // ---- work item: (batch, head, split, q-tile), q-tile fastest, XCD-aware order
-  const uint32_t id = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = id % a.n_qtiles;
-  uint32_t rest = id / a.n_qtiles;
-  const int split = rest % a.splits;
-  rest /= a.splits;
-  const int h = rest % a.H;
-  const int b = rest / a.H;
+  // ---- work item (piece, unit). With a work queue the items are handed out at run time;
+  // without, workgroup i takes item i / 8 of XCD i % 8 (workgroups reach the XCDs round-robin).
+  const uint32_t U = (uint32_t)a.n_qtiles * a.H * a.B;
+  uint32_t id;
+  {
+    __shared__ int s_item;
+    if (a.queue != nullptr) {
+      if (threadIdx.x == 0) s_item = take_item(a.queue, U, a.splits, blockIdx.x & 7u);
+      __syncthreads();
+    } else if (threadIdx.x == 0) {
+      uint32_t st, n;
+      xcd_units(U, blockIdx.x & 7u, st, n);
+      const uint32_t j = blockIdx.x >> 3;
+      s_item = j < a.splits * n ? (int)((j / n) * U + st + j % n) : -1;
+    }
+    __syncthreads();
+    const int item = s_item;
+    if (item < 0) return;  // every wave of the workgroup
+    id = (uint32_t)item;
+  }
+  const int split = id / U;
+  const uint32_t unit = id % U;
+  const int qt = unit % a.n_qtiles;
+  const int h = (unit / a.n_qtiles) % a.H;
+  const int b = unit / ((uint32_t)a.n_qtiles * a.H);
 
   const int q0 = qt * BM + wave * 32;  // first query of this wave (wave-uniform)
   const bool wave_active = q0 < a.Lq;
@@ -189,9 +238,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   }
   const int64_t lo = a.lo;
   const int n_tiles = hi > lo ? count_tiles(a, lo, hi) : 0;
-  const int per_split = (n_tiles + a.splits - 1) / a.splits;
-  const int t0 = split * per_split;
-  const int t1 = min(n_tiles, t0 + per_split);
+  // this piece's tiles
+  const int t0 = (int)((int64_t)n_tiles * split / a.splits);
+  const int t1 = (int)((int64_t)n_tiles * (split + 1) / a.splits);
 
   // ---- per-lane LDS offsets
   // DMA: this wave fills 1 KB blocks NDMA*wave + i of each tile; lane -> (row, physical chunk).
@@ -677,7 +726,15 @@ static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
   static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
-  const uint32_t nwg = (uint32_t)a.n_qtiles * a.splits * a.H * a.B;
+  const uint32_t U = (uint32_t)a.n_qtiles * a.H * a.B;
+  const uint32_t per_xcd = a.splits * ((U + 7u) / 8u);  // items of the largest XCD share
+  uint32_t nwg = 8u * per_xcd;
+  if (a.queue != nullptr) {
+    // spare workgroups, 1/16 of an XCD's share (at least one each): enough for the measured
+    // spread of XCD speeds (a few percent)
+    nwg += 8u * ((per_xcd + 15u) / 16u);
+    hipLaunchKernelGGL(attn_queue_reset_kernel, dim3(1), dim3(64), 0, stream, a.queue);
+  }
   hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
                      stream, a);
   return hipGetLastError();

@@ -112,9 +112,13 @@ int choose_splits(int64_t bh, int lq, int bm, int64_t ntiles, int cus) {
   return best_s;
 }
 
+constexpr size_t kQueueBytes = 256;  // 8 work-queue counters, padded
+
 struct Plan {
   AttnKernelArgs a;
   int splits;
+  size_t part_bytes;  // split partials
+  size_t queue_off;   // work-queue counters
   size_t ws_bytes;
 };
 
@@ -214,7 +218,10 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
     }
   }
   plan->splits = splits;
-  plan->ws_bytes = splits > 1 ? (size_t)splits * a.B * a.H * a.Lq * (p->head_dim + 2) * sizeof(float) : 0;
+  // [split partials][work-queue counters at a 256-byte boundary]
+  plan->part_bytes = splits > 1 ? (size_t)splits * a.B * a.H * a.Lq * (p->head_dim + 2) * sizeof(float) : 0;
+  plan->queue_off = (plan->part_bytes + 255) & ~(size_t)255;
+  plan->ws_bytes = plan->queue_off + kQueueBytes;
   a.splits = splits;
   return LBW_OK;
 }
@@ -231,8 +238,12 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
     a.mult_raw = (float)(log(mult) / (double)a.scale);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool ws_ok = ws != nullptr && ws_bytes >= plan.ws_bytes && aligned16(ws);
+  if (ws_ok) {
+    a.queue = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(ws) + plan.queue_off);
+  }
   if (plan.splits > 1) {
-    if (ws == nullptr || ws_bytes < plan.ws_bytes || !aligned16(ws))
+    if (!ws_ok)
       return fail(LBW_ERR_WORKSPACE, "workspace of %zu bytes needed (got %zu)", plan.ws_bytes, ws_bytes);
     const size_t rows = (size_t)plan.splits * a.B * a.H * a.Lq;
     float* base = static_cast<float*>(ws);

@@ -72,15 +72,6 @@ __device__ __forceinline__ float wave_reduce_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// XCD-aware remap of a linear workgroup id. Workgroups are dispatched round-robin over the 8
-// XCDs (id % 8); the remap gives each XCD a contiguous range of logical ids, so logical
-// neighbours (which share K/V) run on the same XCD and share its L2.
-__device__ __forceinline__ uint32_t xcd_remap(uint32_t id, uint32_t n) {
-  const uint32_t xcd = id % 8u, local = id / 8u;
-  const uint32_t per = n / 8u, rem = n % 8u;
-  return xcd * per + (xcd < rem ? xcd : rem) + local;
-}
-
 template <typename T>
 __device__ __forceinline__ T* lds_ptr(unsigned char* base, int byte_off) {
   return reinterpret_cast<T*>(base + byte_off);
