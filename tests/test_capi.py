@@ -128,6 +128,32 @@ def _split_count(H, LQ, LK):
     return n // (LQ * H * 130 * 4)
 
 
+def test_workspace_layout_without_gpu():
+    """Workspace = split partials (splits x rows x (D + 2) fp32) rounded up to 256 bytes, then
+    256 bytes of work-queue counters; a single-pass plan needs only the counters."""
+    from lbw_amd import _lib
+    lib = _lib.load()
+    for H, LQ, LK in [(2, 256, 1024), (40, 3600, 46800), (40, 4680, 32760), (12, 4680, 14040)]:
+        p = _lib.AttnParams()
+        p.batch, p.heads, p.head_dim, p.lq = 1, H, 128, LQ
+        p.q = p.out = 256
+        p.q_stride_b = p.o_stride_b = LQ * H * 128
+        p.q_stride_l = p.o_stride_l = H * 128
+        p.q_stride_h = p.o_stride_h = 128
+        p.n_segments = 1
+        sg = p.seg[0]
+        sg.k = sg.v = 256
+        sg.len = LK
+        sg.k_stride_b = sg.v_stride_b = LK * H * 128
+        sg.k_stride_l = sg.v_stride_l = H * 128
+        sg.k_stride_h = sg.v_stride_h = 128
+        p.kv_lo, p.kv_hi = 0, -1
+        n = lib.lbw_attention_workspace_size(ctypes.byref(p))
+        splits = _split_count(H, LQ, LK)
+        parts = splits * LQ * H * 130 * 4 if splits > 1 else 0
+        assert n == ((parts + 255) // 256) * 256 + 256, (H, LQ, LK, n, splits)
+
+
 def test_segment_length_limit_without_gpu():
     """Segments longer than 2^30 keys are refused before any HIP call (32-bit key indices)."""
     from lbw_amd import _lib
