@@ -102,6 +102,28 @@ def test_split_kv_merge_matches_single_pass(lib, splits):
     assert (one.float() - many.float()).abs().max() < 4e-3
 
 
+@pytest.mark.parametrize("B,Lq,H,Lk,splits", [
+    (1, 40, 1, 700, 3),      # one unit: seven XCD queues empty, their workgroups take from XCD 0
+    (1, 300, 3, 900, 2),     # six units, ragged last q-tile
+    (2, 513, 3, 333, 5),     # batch 2, 18 units, pieces of 1-2 tiles
+    (1, 256, 5, 130, 7),     # more pieces than tiles: empty pieces merge as nothing
+    (3, 100, 7, 2000, 1),    # 21 units, single pass through the queues
+])
+def test_work_queue_covers_every_item(lib, B, Lq, H, Lk, splits):
+    """The per-XCD work queues with stealing hand every (piece, batch, head, q-tile) item to
+    exactly one workgroup for unit counts below, at and above the XCD count, with pieces that
+    hold no tiles, and with batch > 1."""
+    from lbw_amd import attention_segments
+    q, ks, vs = _case(B, Lq, H, [Lk], seed=B * 1000 + Lq + splits)
+    # V halved (exact in bf16): with a few hundred keys a peaked head copies single V rows, and
+    # |o| >= 4 would put one bf16 output rounding above the 1e-2 bound
+    v = (vs[0].float() * 0.5).to(torch.bfloat16)
+    out = attention_segments(q.to(DEV), [(ks[0].to(DEV), v.to(DEV))], num_splits=splits)
+    ref = O.attention_ref(q, ks[0], v)
+    print(f"queue case B={B} Lq={Lq} H={H} Lk={Lk} splits={splits}", metrics(out, ref))
+    assert_parity(out, ref, f"B={B} Lq={Lq} H={H} Lk={Lk} splits={splits}")
+
+
 @pytest.mark.parametrize("jump", [2.0, 12.0, 60.0])
 def test_exponent_reference_moves_mid_row(lib, jump):
     """Scores that rise tile after tile (by `jump` natural-log units per 64-key tile along one
