@@ -22,7 +22,8 @@ import torch
 from . import _lib
 
 __all__ = ["attention", "flash_attention", "exact_attention", "exact_attention_chunks",
-           "cross_attention", "attention_partial", "attention_merge", "attention_segments",
+           "cross_attention", "attention_partial", "attention_merge", "attention_chain",
+           "attention_segments",
            "window_from_mask"]
 
 _ws_cache: dict = {}
@@ -286,6 +287,27 @@ def attention_merge(parts, out: torch.Tensor | None = None) -> torch.Tensor:
                                       out.stride(1), out.stride(2), _lib.stream_ptr(device)),
                    "lbw_attn_merge")
     return out
+
+
+def attention_chain(q, segments, chain=None, normalize=False, *, kv_lo=None, kv_hi=None,
+                    softmax_scale=None, out: torch.Tensor | None = None):
+    """cte_call's chain contract (attention.py:654-694): a call over ``segments`` continues the
+    online softmax of the earlier calls in ``chain`` (same q, other keys); the call with
+    ``normalize=True`` returns the attention over the union of every call's keys, bf16
+    ``[B, Lq, N, D]``. Without it the call returns the new chain state.
+
+    The state is the tuple of the calls' partials ``(O, m, l)`` (attention_partial), combined
+    exactly by one log-sum-exp merge at the normalizing call, where the reference carries one
+    running (O, -max, sum) triple; the result is the same softmax. At most 16 calls."""
+    parts = tuple(chain) if chain is not None else ()
+    if segments:
+        parts = parts + (attention_partial(q, segments, kv_lo=kv_lo, kv_hi=kv_hi,
+                                           softmax_scale=softmax_scale),)
+    if not normalize:
+        return parts
+    if not parts:
+        raise ValueError("a chain needs at least one call with keys")
+    return attention_merge(parts, out=out)
 
 
 def default_scale(head_dim: int) -> float:

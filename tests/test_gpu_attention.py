@@ -167,6 +167,22 @@ def test_partials_match_oracle_and_merge(lib):
     assert_parity(merged, ref, "merge")
 
 
+def test_chain_over_key_sets_equals_union(lib):
+    """cte_call's chain (attention.py:654-694): calls over the cached chunks, then the new
+    chunk, continue one softmax; the normalizing call equals attention over all the keys."""
+    from lbw_amd import attention_chain
+    q, ks, vs = _case(1, 300, 3, [700, 450, 300], seed=11)
+    segs = [(k.to(DEV), v.to(DEV)) for k, v in zip(ks, vs)]
+    state = attention_chain(q.to(DEV), segs[:2])          # cached chunks (two segments)
+    state = attention_chain(q.to(DEV), segs[2:3], state)  # the new chunk
+    out = attention_chain(q.to(DEV), [], state, normalize=True)
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1))
+    assert_parity(out, ref, "chain")
+    # the same keys in one call
+    one = attention_chain(q.to(DEV), segs, normalize=True)
+    assert (one.float() - out.float()).abs().max() < 4e-3
+
+
 def test_cross_attention_masked_and_unmasked(lib):
     from lbw_amd import attention, cross_attention
     g = torch.Generator().manual_seed(7)
