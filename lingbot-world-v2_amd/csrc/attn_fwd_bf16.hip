@@ -518,7 +518,27 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         return l;
       };
       float ls = exps();
+      // schedule of the step's block, which the groups must share with the MFMAs (ahead of the
+      // redo branch below): the first pairs' fragments, then per MFMA pair: MFMA, 2 VALU, the LDS
+      // reads of the pair K_AHEAD / V_AHEAD ahead, MFMA, 2 VALU; the rest of the VALU work is
+      // left to the compiler. Measured against the compiler's own order and against 1, 3 or 4
+      // VALU per MFMA and other places for the reads: 3.5 % faster than the next best.
+      constexpr int NDS0 = (KPRE ? 0 : K_AHEAD) + (VPRE ? 0 : 2 * V_AHEAD);
+      if constexpr (NDS0 > 0) __builtin_amdgcn_sched_group_barrier(0x100, NDS0, 0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool rk = i + K_AHEAD < 8 || NKO >= 0, rv = i + V_AHEAD < 8 || NVO >= 0;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // 2 VALU
+        if (rk && rv) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // LDS reads
+        else if (rv) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        else if (rk) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+      }
       if constexpr (!TRACK) {
+        // P is packed in this block, not in the redo branch's successors
+        asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(ls));
         // softmax, part 3: a row sum beyond 2^16 (or not finite) means some p outgrew the
         // reference. Rare after a row's first tiles: move the reference to the row max of
         // this sub-block (and the old reference), redo the exponentials, and rescale O and l
@@ -540,25 +560,6 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       lsum = __builtin_fmaf(lsum, alpha, ls);
       // keep the exponentials in this step's block (not sunk into the next one)
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
-      // schedule: the first pairs' fragments, then per MFMA pair: MFMA, 4 VALU, MFMA, 4 VALU,
-      // the LDS reads of the pairs K_AHEAD / V_AHEAD ahead (the VALU work spread over the
-      // whole step measured faster than larger groups that finish it early). This shapes the
-      // TRACK step only: without TRACK these groups fall after the redo branch, in a block
-      // with no MFMAs, and the compiler's own order of the step (measured 2 % faster than
-      // this pattern placed ahead of the branch) stands.
-      constexpr int NDS0 = (KPRE ? 0 : K_AHEAD) + (VPRE ? 0 : 2 * V_AHEAD);
-      if constexpr (NDS0 > 0) __builtin_amdgcn_sched_group_barrier(0x100, NDS0, 0);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
-        const bool rk = i + K_AHEAD < 8 || NKO >= 0, rv = i + V_AHEAD < 8 || NVO >= 0;
-        if (rk && rv) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-        else if (rv) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        else if (rk) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
       pend = move;
       alpha_p = alpha;
     };
