@@ -575,6 +575,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       constexpr int SN = (ST + 1) % NSTAGE;           // stage of tile u+1
       const int vrow = vr[0];
       const float sk = skr[0], sv = svr[0];
+      if constexpr (FP8) {
+        // tile u+1 (loaded one tile ago) into its stage, the one tile u-2 left: free since the
+        // last barrier and not read before the next one, so the writes can overlap step 2u
+        if (u >= 1 && u + 1 < T) write8(SN);
+      }
       // step 2u reads the V fragments of step 2u+1 (tile u, already resident); step 2u+1 reads
       // those of step 2u+2 (tile u+1 rows 32..63, resident since the barrier, and tile u)
       if (wave_active)
@@ -583,8 +588,6 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
              std::true_type{}, std::integral_constant<int, -1>{},
              std::integral_constant<int, ST * TILE_B>{}, sA, sB, pA, pB, 0, vrow, sk, sv);
       if constexpr (FP8) {
-        // tile u+1 (loaded one tile ago) into its stage, the one tile u-2 left
-        if (u >= 1 && u + 1 < T) write8(SN);
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the LDS writes are done
       } else {
         if (u + 1 < T) wait_tiles_outstanding(min(NSTAGE - 3, T - 2 - u));
