@@ -84,16 +84,18 @@ def build_layers(n_layers, dev):
 
 
 def run_layer(L, tabs, ev=None):
-    from lbw_amd import attention_segments, qk_norm_rope_
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments, prescaled_q_scale, qk_norm_rope_
     slot = slice(LK - LQ, LK)
     if ev is not None:
         ev[0].record()
     qk_norm_rope_(L["xq"], L["xk"], None, None, L["wq"], L["wk"], tabs, EPS, H, q_out=L["q"],
                   k_out=L["cache_k"][0, slot].view(LQ, C), v=L["xv"],
-                  v_out=L["cache_v"][0, slot].view(LQ, C))
+                  v_out=L["cache_v"][0, slot].view(LQ, C), q_scale=prescaled_q_scale(D))
     if ev is not None:
         ev[1].record()
-    attention_segments(L["q"].view(1, LQ, H, D), [(L["cache_k"], L["cache_v"])], out=L["out"])
+    # q carries log2(e)/sqrt(D) (the reference's pre-scaled q, model_fast.py:1233): folded softmax
+    attention_segments(L["q"].view(1, LQ, H, D), [(L["cache_k"], L["cache_v"])], out=L["out"],
+                       softmax_scale=PRESCALED_SOFTMAX_SCALE)
     if ev is not None:
         ev[2].record()
 

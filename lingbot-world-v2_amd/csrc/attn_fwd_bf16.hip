@@ -33,9 +33,9 @@
 // VALU and MFMA work of one wave overlap; the second wave on the SIMD fills what is left.
 //
 // Online softmax in base 2 with the scale folded into one FMA: p = exp2(s*c - m*c),
-// c = scale*log2(e). The exponent reference m is only raised when the running max exceeds it
-// by more than 8 (log2 units), so P <= 256 and the O rescale is skipped on almost every step;
-// O and l share the reference, so the final O / l is exact.
+// c = scale*log2(e), against an exponent reference m that moves lazily (the redo in the step);
+// O and l share the reference, so the final O / l is exact. With a pre-scaled q (c == 1) the
+// QK chain starts from -m and p = exp2(S) directly.
 
 #include "attn_tiles.h"
 
@@ -177,9 +177,13 @@ __global__ void __launch_bounds__(64) attn_queue_reset_kernel(uint32_t* q) {
 // converted exactly to bf16 (every e4m3 value is a bf16 value) and written into the same LDS
 // layout; the block scales fold into the softmax (K's into the exponent's multiplier, V's into
 // its addend as log2, and out of the row sum), so the MFMA loop is the bf16 one.
-template <bool FP8, bool TRACK>
+// FOLD: scale * log2(e) == 1, i.e. q already carries log2(e)/sqrt(d) (a pre-scaled q, as the
+// fused q/k kernel writes it): the QK chain starts from -m instead of 0, so the MFMA result is
+// already the exponent of p and the softmax needs no per-score FMA (see the step).
+template <bool FP8, bool TRACK, bool FOLD>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
+  static_assert(!FOLD || (!FP8 && !TRACK), "the folded softmax is the plain bf16 form");
   constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
@@ -279,6 +283,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
   float m_used = M_INIT, m_true = -INFINITY, lsum = 0.0f;  // exponent ref, row max, row sum
   const float c = a.scale_log2;
+  // FOLD: the exponent reference (log2 units, c = 1), and whether this row's has been set from a
+  // valid score yet (before that, its O and l are 0)
+  float mref = 0.0f;
+  bool mset = false;
   const float mult_raw = sreg(a.mult_raw);
   // the call carries a multiplicity bias (mult_key >= 0: the sign of its high word)
   const int mult = sreg((int)(a.mult_key >> 32)) >= 0;
@@ -398,9 +406,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     // copying: S of the sub-block being softmaxed / being computed, P of the previous / current
     // sub-block. `pend` / `alpha_p`: an O rescale decided by the previous step, applied at the
     // start of the next one (after the PV MFMAs that still used the old reference).
-    floatx16 sA, sB;
+    floatx16 sA, sB, cinit;  // cinit (FOLD): -mref, the start of every QK chain
 #pragma unroll
-    for (int r = 0; r < 16; ++r) { sA[r] = 0.0f; sB[r] = 0.0f; }
+    for (int r = 0; r < 16; ++r) { sA[r] = 0.0f; sB[r] = 0.0f; cinit[r] = 0.0f; }
     u32x4 pA[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
     u32x4 pB[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
     bool pend = false;
@@ -490,8 +498,12 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       const float lsv = FP8 ? __builtin_amdgcn_logf(sv) : 0.0f;
       float ca = lsv - m_used * c;
       // MFMAs of the neighbouring sub-blocks
+      if constexpr (FOLD) {
+        s_out = cinit;
+      } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s_out[r] = 0.0f;
+        for (int r = 0; r < 16; ++r) s_out[r] = 0.0f;
+      }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (i + K_AHEAD < 8) load_k(koff_c, i + K_AHEAD);
@@ -508,8 +520,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         for (int m = 0; m < 2; ++m) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], cm, ca));
-            const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], cm, ca));
+            const float x0 = fast_exp2(FOLD ? s_in[8 * m + 2 * e] : __builtin_fmaf(s_in[8 * m + 2 * e], cm, ca));
+            const float x1 = fast_exp2(FOLD ? s_in[8 * m + 2 * e + 1]
+                                            : __builtin_fmaf(s_in[8 * m + 2 * e + 1], cm, ca));
             p_out[m][e] = pack_bf16x2(x0, x1);
             l = (m == 0 && e == 0) ? x0 + x1 : l + (x0 + x1);
           }
@@ -528,15 +541,58 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const bool rk = i + K_AHEAD < 8 || NKO >= 0, rv = i + V_AHEAD < 8 || NVO >= 0;
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // 2 VALU
+        if constexpr (FOLD) {
+          // (the VALU class does not take the exponentials, which without the FMAs would
+          // otherwise bunch at the start of the step: one per MFMA, named as transcendentals)
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);  // 1 exponential
+          __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // 1 VALU
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // 2 VALU
+        }
         if (rk && rv) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // LDS reads
         else if (rv) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         else if (rk) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        if constexpr (FOLD) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+        }
       }
-      if constexpr (!TRACK) {
+      if constexpr (FOLD) {
+        asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(ls));
+        // s_in is s - mref. Redo as below, and also while a row's reference is not yet set
+        // (it starts at 0; the row's O and l are still 0 then, so it may move down, with no
+        // rescale). mx is the row's (lanes l and l^32 agree), so both lanes move alike.
+        if (__any(!mset || !(ls <= P_LIMIT))) {
+          float mx = s_in[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+          mx = wave_max_xor32(mx);
+          float d;  // the reference's move, log2 units
+          if (mset) {
+            d = fmaxf(mx, 0.0f);
+            alpha = fast_exp2(-d);
+          } else {
+            mset = mx > -INFINITY;  // a fully masked sub-block leaves it unset
+            d = mset ? mx : 0.0f;
+          }
+          move = true;
+          mref += d;
+          // s_out (the next sub-block, started from the old -mref in this step) moves too
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            s_in[r] -= d;
+            s_out[r] -= d;
+            cinit[r] = -mref;
+          }
+          ls = exps();
+        }
+      } else if constexpr (!TRACK) {
         // P is packed in this block, not in the redo branch's successors
         asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(ls));
         // softmax, part 3: a row sum beyond 2^16 (or not finite) means some p outgrew the
@@ -685,6 +741,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       if constexpr (TRACK) {
         f = fast_exp2((m_used - m_true) * c);
         m_out = m_true * a.scale;
+      } else if constexpr (FOLD) {
+        m_out = mref * a.scale;
       } else {
         m_out = m_used * a.scale;
       }
@@ -725,9 +783,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-template <bool FP8, bool TRACK>
+template <bool FP8, bool TRACK, bool FOLD = false>
 static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK>,
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t U = (uint32_t)a.n_qtiles * a.H * a.B;
@@ -739,13 +797,15 @@ static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
     nwg += 8u * ((per_xcd + 15u) / 16u);
     hipLaunchKernelGGL(attn_queue_reset_kernel, dim3(1), dim3(64), 0, stream, a.queue);
   }
-  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
                      stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
-  return a.track_max ? launch<false, true>(a, stream) : launch<false, false>(a, stream);
+  if (a.track_max) return launch<false, true>(a, stream);
+  // a pre-scaled q (scale * log2(e) exactly 1 in fp32) takes the folded softmax
+  return a.scale_log2 == 1.0f ? launch<false, false, true>(a, stream) : launch<false, false>(a, stream);
 }
 
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {

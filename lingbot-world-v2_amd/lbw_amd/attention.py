@@ -23,8 +23,8 @@ from . import _lib
 
 __all__ = ["attention", "flash_attention", "exact_attention", "exact_attention_chunks",
            "cross_attention", "attention_partial", "attention_merge", "attention_chain",
-           "attention_segments",
-           "window_from_mask"]
+           "attention_segments", "window_from_mask", "PRESCALED_SOFTMAX_SCALE",
+           "prescaled_q_scale"]
 
 _ws_cache: dict = {}
 
@@ -312,3 +312,18 @@ def attention_chain(q, segments, chain=None, normalize=False, *, kv_lo=None, kv_
 
 def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+LOG2E = 1.4426950408889634
+# Softmax scale for a q that already carries log2(e)/sqrt(d) (``prescaled_q_scale``): then
+# scale * log2(e) is exactly 1 in fp32 and the kernel takes its folded softmax, which needs no
+# per-score scaling. The pre-scale is the reference's own (model_fast.py:1233, 2666-2676: q
+# pre-scaled by 1/sqrt(d) in bf16 by the fused norm + RoPE kernel), with log2(e) folded in too.
+PRESCALED_SOFTMAX_SCALE = math.log(2.0)
+
+
+def prescaled_q_scale(head_dim: int) -> float:
+    """The q scale for the fused q/k kernel's output that pairs with
+    ``softmax_scale=PRESCALED_SOFTMAX_SCALE``: softmax(q k^T / sqrt(d)) unchanged, up to one bf16
+    rounding of the scaled q."""
+    return LOG2E / math.sqrt(head_dim)

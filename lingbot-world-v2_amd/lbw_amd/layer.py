@@ -16,7 +16,8 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from .attention import attention_segments, cross_attention, padding_start
+from .attention import (PRESCALED_SOFTMAX_SCALE, attention_segments, cross_attention,
+                        padding_start, prescaled_q_scale)
 from .chunked_kv_cache import FlatKVCache, chunk_routing, ordered_chunks
 from .fp8 import attention_fp8kv, quantize_kv_fp8
 from .qk_post import qk_norm_rope_
@@ -52,8 +53,9 @@ class WanSelfAttention:
         self.gq, self.gk = gq, gk
         self.freqs = wan_rope_freqs(self.head_dim) if freqs is None else freqs
 
-    def _project_norm_rope(self, x, grid, start_frame, k_out, v_out):
-        """x [1, L, C] -> q' [L, C] (bf16) and K/V written into k_out / v_out ([L, C] views)."""
+    def _project_norm_rope(self, x, grid, start_frame, k_out, v_out, q_scale=1.0):
+        """x [1, L, C] -> q' [L, C] (bf16, times q_scale) and K/V written into k_out / v_out
+        ([L, C] views)."""
         L = x.shape[1]
         qkv = F.linear(x[0], self.w_qkv, self.b_qkv)                    # [L, 3C] bf16
         C = self.C
@@ -61,7 +63,7 @@ class WanSelfAttention:
         tabs = causal_rope_tables(self.freqs, grid, start_frame, device=x.device)
         q = torch.empty(L, C, dtype=torch.bfloat16, device=x.device)
         qk_norm_rope_(q_raw, k_raw, self.bq, self.bk, self.gq, self.gk, tabs, self.eps,
-                      self.heads, q_out=q, k_out=k_out, v=v, v_out=v_out)
+                      self.heads, q_out=q, k_out=k_out, v=v, v_out=v_out, q_scale=q_scale)
         return q
 
     def prefill(self, x, grid, start_frame, cache: FlatKVCache, current_start: int = 0):
@@ -80,11 +82,13 @@ class WanSelfAttention:
         p = cache.plan(current_start, L)
         cache.apply_roll(p)
         ks, vs = cache.slot(p)
+        # q pre-scaled by log2(e)/sqrt(d) in the norm kernel: the attention's folded softmax
         q = self._project_norm_rope(x, grid, start_frame, ks[0].view(L, self.C),
-                                    vs[0].view(L, self.C))
+                                    vs[0].view(L, self.C), prescaled_q_scale(self.head_dim))
         cache.commit(p)
         o = attention_segments(q.view(1, L, self.heads, self.head_dim), [(cache.k, cache.v)],
-                               kv_lo=p.attn_lo, kv_hi=p.attn_hi)
+                               kv_lo=p.attn_lo, kv_hi=p.attn_hi,
+                               softmax_scale=PRESCALED_SOFTMAX_SCALE)
         return F.linear(o.view(1, L, self.C), self.wo, self.bo)
 
     def forward_chunked(self, x, grid, start_frame, chunks, chunk_index: int):
@@ -97,9 +101,10 @@ class WanSelfAttention:
         if kd.shape[1] != L:
             raise ValueError(f"chunk buffers hold {kd.shape[1]} tokens, the chunk has {L}")
         q = self._project_norm_rope(x, grid, start_frame, kd[0].view(L, self.C),
-                                    vd[0].view(L, self.C))
+                                    vd[0].view(L, self.C), prescaled_q_scale(self.head_dim))
         kk, vv = ordered_chunks(chunks, dest, leading)
-        o = attention_segments(q.view(1, L, self.heads, self.head_dim), list(zip(kk, vv)))
+        o = attention_segments(q.view(1, L, self.heads, self.head_dim), list(zip(kk, vv)),
+                               softmax_scale=PRESCALED_SOFTMAX_SCALE)
         return F.linear(o.view(1, L, self.C), self.wo, self.bo)
 
 

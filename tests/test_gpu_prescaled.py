@@ -1,0 +1,113 @@
+"""GPU parity of the folded softmax: q pre-scaled by log2(e)/sqrt(d) with softmax scale ln 2
+(scale * log2(e) == 1 in fp32), the pairing the fused q/k kernel and the Wan layers use. The
+kernel then starts each QK chain from -m instead of scaling every score, and sets each row's
+exponent reference from its first valid sub-block. Checked against the fp32 oracle on the same
+pre-scaled bf16 q, over the shapes of the plain-scale tests: windows, ragged and empty segments,
+rows with no keys, KV splits through the work queues, references that move mid-row, and
+peaked heads."""
+import math
+
+import pytest
+import torch
+
+import oracle as O
+from parity import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+LN2 = math.log(2.0)
+
+
+def _prescaled(q):
+    from lbw_amd import prescaled_q_scale
+    return (q.float() * prescaled_q_scale(q.shape[-1])).to(torch.bfloat16)
+
+
+def _case(B, Lq, H, seg_lens, seed):
+    g = torch.Generator().manual_seed(seed)
+    gains = torch.tensor([0.25, 0.5, 1.0, 2.0, 4.0, 8.0, 16.0, 1.0])[torch.arange(H) % 8]
+    q = (torch.randn(B, Lq, H, 128, generator=g) * gains.view(1, 1, H, 1)).to(torch.bfloat16)
+    ks = [torch.randn(B, L, H, 128, generator=g).to(torch.bfloat16) for L in seg_lens]
+    # V halved (exact): peaked heads copy single V rows, and |o| >= 4 would put one bf16
+    # output rounding above the 1e-2 bound
+    vs = [(torch.randn(B, L, H, 128, generator=g) * 0.5).to(torch.bfloat16) for L in seg_lens]
+    return _prescaled(q), ks, vs
+
+
+def test_scale_pairing_is_exactly_one():
+    """The host takes the folded kernel when scale * log2(e) rounds to 1.0 in fp32."""
+    import numpy as np
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE
+    assert np.float32(PRESCALED_SOFTMAX_SCALE) * np.float32(1.4426950408889634) == np.float32(1.0)
+
+
+@pytest.mark.parametrize("B,Lq,H,seg_lens,window,splits", [
+    (1, 300, 2, [1000], None, 0),
+    (1, 37, 3, [64], None, 0),
+    (1, 1, 1, [1], None, 0),
+    (1, 257, 2, [65], None, 0),
+    (2, 129, 2, [100, 37, 200, 5], (50, 300), 0),
+    (1, 512, 7, [4096, 1560], (1000, 5656), 0),
+    (1, 96, 2, [7, 0, 130], None, 0),
+    (1, 96, 2, [300], (200, 100), 0),       # empty window: every row has no keys -> 0
+    (1, 300, 7, [2000], None, 3),
+    (3, 100, 7, [2000], None, 1),
+    (2, 513, 3, [333], None, 5),
+    (1, 256, 5, [130], None, 7),
+])
+def test_prescaled_matches_oracle(lib, B, Lq, H, seg_lens, window, splits):
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments
+    q, ks, vs = _case(B, Lq, H, seg_lens, seed=Lq + H + splits)
+    lo, hi = (None, None) if window is None else window
+    out = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV)) for k, v in zip(ks, vs)],
+                             kv_lo=lo, kv_hi=hi, softmax_scale=PRESCALED_SOFTMAX_SCALE,
+                             num_splits=splits)
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1), kv_lo=lo, kv_hi=hi,
+                          softmax_scale=LN2)
+    assert_parity(out, ref, f"B={B} Lq={Lq} H={H} segs={seg_lens} window={window} splits={splits}")
+
+
+def test_prescaled_window_starting_mid_tile(lib):
+    """Keys from 100 on: the first tile's first sub-block is masked whole, so the reference stays
+    unset through it and is set from the second."""
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments
+    q, ks, vs = _case(1, 200, 4, [700], seed=5)
+    for lo in (40, 100, 129):
+        out = attention_segments(q.to(DEV), [(ks[0].to(DEV), vs[0].to(DEV))], kv_lo=lo,
+                                 softmax_scale=PRESCALED_SOFTMAX_SCALE)
+        ref = O.attention_ref(q, ks[0], vs[0], kv_lo=lo, softmax_scale=LN2)
+        assert_parity(out, ref, f"lo={lo}")
+
+
+@pytest.mark.parametrize("jump", [2.0, 12.0, 60.0])
+def test_prescaled_reference_moves_mid_row(lib, jump):
+    """Scores that rise by `jump` natural-log units per 64-key tile: the reference moves, and
+    the next sub-block's S, started from the old -m in the same step, moves with it."""
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments
+    g = torch.Generator().manual_seed(31)
+    B, Lq, H, L = 1, 70, 2, 12 * 64 + 17
+    u = torch.randn(128, generator=g)
+    u = u / u.norm()
+    q = (torch.randn(B, Lq, H, 128, generator=g) * 0.3 + 4.0 * u).to(torch.bfloat16)
+    ramp = torch.arange(L, dtype=torch.float32).div(64).floor()
+    gain = (ramp * jump * math.sqrt(128) / 4.0).view(1, L, 1, 1)
+    k = (torch.randn(B, L, H, 128, generator=g) * 0.3 + gain * u).to(torch.bfloat16)
+    v = (torch.randn(B, L, H, 128, generator=g) * 0.5).to(torch.bfloat16)
+    qs = _prescaled(q)
+    ref = O.attention_ref(qs, k, v, softmax_scale=LN2)
+    for splits in (1, 3):
+        out = attention_segments(qs.to(DEV), [(k.to(DEV), v.to(DEV))], num_splits=splits,
+                                 softmax_scale=PRESCALED_SOFTMAX_SCALE)
+        assert_parity(out, ref, f"jump {jump} splits {splits}")
+
+
+def test_prescaled_equals_plain_kernel(lib):
+    """The folded kernel and the plain one (scale ln 2 (1 + 2^-21): c != 1 in fp32, the FMA
+    path) on the same pre-scaled q agree to bf16 rounding."""
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments
+    q, ks, vs = _case(1, 400, 6, [1500], seed=77)
+    segs = [(ks[0].to(DEV), vs[0].to(DEV))]
+    fold = attention_segments(q.to(DEV), segs, softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    plain = attention_segments(q.to(DEV), segs, softmax_scale=LN2 * (1 + 2.0 ** -21))
+    assert (fold.float() - plain.float()).abs().max() < 8e-3
