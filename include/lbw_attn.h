@@ -72,7 +72,9 @@ typedef struct lbw_attn_params {
   lbw_kv_segment seg[LBW_MAX_KV_SEGMENTS];
   int64_t kv_lo, kv_hi; /* window [kv_lo, kv_hi) over the concatenated keys; kv_hi < 0: all */
   const int32_t* k_lens;/* device int32 [B] valid key counts (masked cross-attention) or NULL */
-  float softmax_scale;  /* <= 0: 1 / sqrt(head_dim) */
+  float softmax_scale;  /* <= 0: 1 / sqrt(head_dim). ln 2 (softmax_scale * log2(e) == 1 in
+                         * fp32) marks a q pre-scaled by log2(e) / sqrt(head_dim): the bf16
+                         * kernel then needs no per-score scaling (its fastest form) */
   int32_t num_splits;   /* KV splits merged by log-sum-exp; 0 = choose, 1 = single pass */
   /* Optional cte_partial outputs, fp32 and contiguous: O_unnorm [B, H, Lq, D],
    * m [B, H, Lq] (row max of the scaled scores), l [B, H, Lq] (row sum of exp(s - m)).
