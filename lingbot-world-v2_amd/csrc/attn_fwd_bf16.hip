@@ -286,7 +286,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   // FOLD: the exponent reference (log2 units, c = 1), and whether this row's has been set from a
   // valid score yet (before that, its O and l are 0)
   float mref = 0.0f;
-  bool mset = false;
+  float mlim = -1.0f;  // the redo threshold of this row: -1 until its reference is set, then P_LIMIT
   const float mult_raw = sreg(a.mult_raw);
   // the call carries a multiplicity bias (mult_key >= 0: the sign of its high word)
   const int mult = sreg((int)(a.mult_key >> 32)) >= 0;
@@ -568,18 +568,19 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         // s_in is s - mref. Redo as below, and also while a row's reference is not yet set
         // (it starts at 0; the row's O and l are still 0 then, so it may move down, with no
         // rescale). mx is the row's (lanes l and l^32 agree), so both lanes move alike.
-        if (__any(!mset || !(ls <= P_LIMIT))) {
+        if (__any(!(ls <= mlim))) {
           float mx = s_in[0];
 #pragma unroll
           for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
           mx = wave_max_xor32(mx);
           float d;  // the reference's move, log2 units
-          if (mset) {
+          if (mlim > 0.0f) {
             d = fmaxf(mx, 0.0f);
             alpha = fast_exp2(-d);
           } else {
-            mset = mx > -INFINITY;  // a fully masked sub-block leaves it unset
-            d = mset ? mx : 0.0f;
+            const bool set = mx > -INFINITY;  // a fully masked sub-block leaves it unset
+            d = set ? mx : 0.0f;
+            mlim = set ? P_LIMIT : -1.0f;
           }
           move = true;
           mref += d;
