@@ -278,6 +278,24 @@ def pmc_workload():
     print("pmc workload done", flush=True)
 
 
+def counter_workload():
+    """The program the SQ counter passes profile: 5 chunk attention calls at the workload's
+    shape with q pre-scaled by log2(e)/sqrt(D) (the folded softmax), on seeded inputs."""
+    import torch
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments, prescaled_q_scale
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = (torch.randn(1, LQ, H, D, generator=g, device=dev) * prescaled_q_scale(D)).to(torch.bfloat16)
+    k = torch.randn(1, LK, H, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(1, LK, H, D, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    for _ in range(5):
+        attention_segments(q, [(k, v)], out=out, softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    torch.cuda.synchronize()
+    print("counter workload done", flush=True)
+
+
 def _pmc_rows(d, counter):
     """Per-dispatch values of `counter` from a rocprofv3 --pmc csv output directory."""
     files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
@@ -356,6 +374,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the timings of the other workload shapes")
+    ap.add_argument("--counter-workload", action="store_true",
+                    help="5 pre-scaled chunk attention calls (the program of the SQ counter passes)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the program profiled by the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -371,6 +391,9 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.counter_workload:
+        counter_workload()
+        return
     if args.pmc_workload:
         pmc_workload()
         return
