@@ -111,3 +111,31 @@ def test_prescaled_equals_plain_kernel(lib):
     fold = attention_segments(q.to(DEV), segs, softmax_scale=PRESCALED_SOFTMAX_SCALE)
     plain = attention_segments(q.to(DEV), segs, softmax_scale=LN2 * (1 + 2.0 ** -21))
     assert (fold.float() - plain.float()).abs().max() < 8e-3
+
+
+def test_prescaled_cross_attention_masked_and_dedup(lib):
+    """The folded kernel on the cross-attention paths: per-batch valid key counts (k_lens) and
+    the exact dedup form, whose multiplicity bias ln(mult) / scale is log2(mult) when
+    scale * log2(e) == 1."""
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments, padding_start
+    g = torch.Generator().manual_seed(43)
+    H, Lq, L, nv = 4, 333, 512, 300
+    q = _prescaled(torch.randn(2, Lq, H, 128, generator=g).to(torch.bfloat16))
+    k = torch.randn(2, L, H, 128, generator=g).to(torch.bfloat16)
+    v = (0.5 * torch.randn(2, L, H, 128, generator=g)).to(torch.bfloat16)
+    k_lens = torch.tensor([300, 512], dtype=torch.int32)
+    out = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV))], k_lens=k_lens.to(DEV),
+                             cross=True, softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    ref = O.attention_ref(q, k, v, k_lens=k_lens, softmax_scale=LN2)
+    assert_parity(out, ref, "masked")
+    # dedup: rows nv.. of k/v identical (one batch)
+    kd = torch.randn(1, L, H, 128, generator=g)
+    vd = 0.5 * torch.randn(1, L, H, 128, generator=g)
+    kd[:, nv:] = torch.randn(1, 1, H, 128, generator=g)
+    vd[:, nv:] = 0.5 * torch.randn(1, 1, H, 128, generator=g)
+    kd, vd = kd.to(torch.bfloat16), vd.to(torch.bfloat16)
+    nd = padding_start(kd.to(DEV), vd.to(DEV))
+    assert nd == nv
+    out = attention_segments(q[:1].to(DEV), [(kd.to(DEV), vd.to(DEV))], cross=True, n_distinct=nd,
+                             softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    assert_parity(out, O.attention_ref(q[:1], kd, vd, softmax_scale=LN2), "dedup")
