@@ -454,7 +454,7 @@ def main():
         "config": {"workload": "wan14b_720p_causal_chunk_selfattn", "layers": len(layers),
                    "heads": H, "head_dim": D, "q_tokens": LQ, "kv_tokens": LK,
                    "grid": list(GRID), "start_frame": START_FRAME,
-                   "per_layer": "qk_norm_rope(+KV commit) -> chunk_attn_fwd"},
+                   "per_layer": "qk_norm_rope(+KV commit, q pre-scaled by log2(e)/sqrt(128)) -> chunk_attn_fwd (softmax scale ln 2: folded softmax)"},
         "ms_per_chunk": round(ms_step, 3),
         "ms_per_layer": round(ms_step / len(layers), 4),
         "attn_ms_per_layer": round(attn_ms, 4),
