@@ -183,3 +183,19 @@ def test_split_plan_for_the_measured_shapes():
     assert _split_count(40, 4680, 32760) == 0
     assert _split_count(12, 4680, 14040) == 0
     assert _split_count(12, 1560, 4680) == 3
+
+
+def test_prescaled_pairing_is_exactly_one_in_fp32():
+    """The host (capi.hip: scale_log2 = scale * 1.4426950408889634f in fp32) takes the folded
+    kernel when that product is exactly 1.0f: PRESCALED_SOFTMAX_SCALE must round so, and
+    prescaled_q_scale(D) * PRESCALED_SOFTMAX_SCALE must be the usual 1/sqrt(D)."""
+    import math
+    import numpy as np
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, prescaled_q_scale
+    assert np.float32(PRESCALED_SOFTMAX_SCALE) * np.float32(1.4426950408889634) == np.float32(1.0)
+    # one ulp either way is the plain kernel
+    up = np.nextafter(np.float32(PRESCALED_SOFTMAX_SCALE), np.float32(1))
+    assert up * np.float32(1.4426950408889634) != np.float32(1.0)
+    for d in (64, 128):
+        assert math.isclose(prescaled_q_scale(d) * PRESCALED_SOFTMAX_SCALE, 1 / math.sqrt(d),
+                            rel_tol=1e-15)
