@@ -132,3 +132,25 @@ def test_prescaled_cross_attention_masked_and_dedup(lib):
     out = attention_segments(q[:1].to(DEV), [(kd.to(DEV), vd.to(DEV))], cross=True, n_distinct=nd,
                              softmax_scale=PRESCALED_SOFTMAX_SCALE)
     assert_parity(out, O.attention_ref(q[:1], kd, vd, softmax_scale=LN2), "dedup")
+
+
+def test_prescaled_partials_and_chain(lib):
+    """The partials API (tracked row max, the FMA form with c = 1) under the pre-scaled pairing:
+    m in scaled units (scale * s) as the oracle's partials, and a chain over key sets equal to
+    attention over their union."""
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_chain, attention_partial
+    g = torch.Generator().manual_seed(51)
+    q = _prescaled(torch.randn(1, 150, 3, 128, generator=g).to(torch.bfloat16))
+    ks = [torch.randn(1, n, 3, 128, generator=g).to(torch.bfloat16) for n in (500, 260)]
+    vs = [(0.5 * torch.randn(1, n, 3, 128, generator=g)).to(torch.bfloat16) for n in (500, 260)]
+    po, pm, pl = attention_partial(q.to(DEV), [(ks[0].to(DEV), vs[0].to(DEV))],
+                                   softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    _, (ro, rm, rl) = O.attention_ref(q, ks[0], vs[0], softmax_scale=LN2, return_partials=True)
+    assert torch.allclose(pm.cpu(), rm, rtol=1e-5, atol=1e-4)
+    assert torch.allclose(pl.cpu(), rl, rtol=5e-3, atol=1e-3)
+    segs = [(k.to(DEV), v.to(DEV)) for k, v in zip(ks, vs)]
+    state = attention_chain(q.to(DEV), segs[:1], softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    state = attention_chain(q.to(DEV), segs[1:], state, softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    out = attention_chain(q.to(DEV), [], state, normalize=True)
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1), softmax_scale=LN2)
+    assert_parity(out, ref, "chain")
