@@ -87,8 +87,14 @@ typedef struct lbw_attn_params {
 /* Bytes of workspace lbw_attention_fwd needs for these params: the split-KV partials (when
  * the call is split) and 256 bytes of work-queue counters, which let the XCDs of the GPU share
  * out the workgroups by speed. A call given no (or too small a) workspace for an unsplit plan
- * still runs, with a static workgroup-to-XCD assignment. */
+ * still runs, with a static workgroup-to-XCD assignment. 0 when the params are invalid (the
+ * attention call then reports why).
+ * A workspace may back only one in-flight call: two calls that may overlap on the device
+ * (e.g. on two streams) need two workspaces. */
 size_t lbw_attention_workspace_size(const lbw_attn_params* p);
+
+/* The same for lbw_attention_fwd_fp8kv (fp8 segments follow the fp8 stride and size rules). */
+size_t lbw_attention_fp8kv_workspace_size(const lbw_attn_params* p);
 
 /* Chunk self-attention: softmax(scale * Q K^T) V over the windowed concatenation of the KV
  * segments, bf16 MFMA, fp32 online softmax. */

@@ -286,6 +286,12 @@ size_t lbw_attention_workspace_size(const lbw_attn_params* p) {
   return plan.ws_bytes;
 }
 
+size_t lbw_attention_fp8kv_workspace_size(const lbw_attn_params* p) {
+  Plan plan;
+  if (make_plan(p, true, &plan) != LBW_OK) return 0;
+  return plan.ws_bytes;
+}
+
 int lbw_attention_fwd(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
                       void* stream) {
   return run_attention(p, false, workspace, workspace_bytes, stream);

@@ -11,8 +11,7 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-# LBW_ATTN_LIB overrides the in-tree library (for comparing builds side by side).
-LIB_PATH = os.environ.get("LBW_ATTN_LIB") or os.path.join(_HERE, "liblbw_attn.so")
+LIB_PATH = os.path.join(_HERE, "liblbw_attn.so")
 
 MAX_KV_SEGMENTS = 8
 FP8_BLOCK = 64
@@ -70,7 +69,8 @@ class QkNormRopeParams(ctypes.Structure):
 
 
 EXPORTS = (
-    "lbw_attention_workspace_size", "lbw_attention_fwd", "lbw_cross_attention_fwd",
+    "lbw_attention_workspace_size", "lbw_attention_fp8kv_workspace_size", "lbw_attention_fwd",
+    "lbw_cross_attention_fwd",
     "lbw_cross_attention_dedup_fwd",
     "lbw_attention_fwd_fp8kv", "lbw_attn_merge", "lbw_qk_norm_rope", "lbw_kv_quant_fp8",
     "lbw_last_error", "lbw_abi_version",
@@ -85,6 +85,8 @@ def _declare(lib):
     vp, i32, i64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
     lib.lbw_attention_workspace_size.argtypes = [P(AttnParams)]
     lib.lbw_attention_workspace_size.restype = ctypes.c_size_t
+    lib.lbw_attention_fp8kv_workspace_size.argtypes = [P(AttnParams)]
+    lib.lbw_attention_fp8kv_workspace_size.restype = ctypes.c_size_t
     lib.lbw_attention_fwd.argtypes = [P(AttnParams), vp, ctypes.c_size_t, vp]
     lib.lbw_attention_fwd.restype = ctypes.c_int
     lib.lbw_cross_attention_fwd.argtypes = [P(AttnParams), vp]

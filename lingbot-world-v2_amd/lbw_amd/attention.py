@@ -29,14 +29,28 @@ __all__ = ["attention", "flash_attention", "exact_attention", "exact_attention_c
 _ws_cache: dict = {}
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """A per-device scratch buffer for split-KV partials, grown on demand (torch allocator)."""
-    key = (device.type, device.index)
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """The scratch buffer (split-KV partials and work-queue counters) of the calls on one
+    stream of one device, grown on demand from torch's caching allocator.
+
+    A workspace may back only one in-flight call: calls on one stream run in order, so one
+    buffer per (device, stream) never serves two kernels at once, while two streams get two
+    buffers. The buffer is allocated with ``stream`` current, so the caching allocator only
+    hands a replaced buffer's memory out again in that stream's order."""
+    key = (device.index, stream)
     buf = _ws_cache.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
         _ws_cache[key] = buf
     return buf
+
+
+def _check_dtype(dtype):
+    """The kernels compute in bf16 (bf16 MFMA, fp32 softmax and accumulators). The reference
+    casts q/k/v to ``dtype`` and runs SDPA in it (attention.py:1134-1141): any other ``dtype``
+    would silently get bf16 accuracy here, so it raises instead."""
+    if dtype != torch.bfloat16:
+        raise NotImplementedError(f"dtype={dtype}: this attention path computes in bfloat16 only")
 
 
 def _as_bf16(t: torch.Tensor) -> torch.Tensor:
@@ -116,8 +130,8 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     if k_lens is not None:
         k_lens = k_lens.to(device=device, dtype=torch.int32).contiguous()
     p = _params(q, out, segs, kv_lo, kv_hi, k_lens, softmax_scale, 1 if cross else num_splits)
-    stream = _lib.stream_ptr(device)
     with torch.cuda.device(device):
+        stream = _lib.stream_ptr(device)
         if cross and n_distinct is not None:
             _lib.check(lib.lbw_cross_attention_dedup_fwd(ctypes_ref(p), int(n_distinct), stream),
                        "lbw_cross_attention_dedup_fwd")
@@ -125,7 +139,7 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
             _lib.check(lib.lbw_cross_attention_fwd(ctypes_ref(p), stream), "lbw_cross_attention_fwd")
         else:
             ws_bytes = lib.lbw_attention_workspace_size(ctypes_ref(p))
-            ws = _workspace(device, ws_bytes) if ws_bytes else None
+            ws = _workspace(device, stream, ws_bytes) if ws_bytes else None
             _lib.check(lib.lbw_attention_fwd(ctypes_ref(p), ws.data_ptr() if ws is not None else None,
                                              ws_bytes, stream), "lbw_attention_fwd")
     return out
@@ -168,7 +182,9 @@ def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=Non
     or 0-d tensors) take precedence over ``attn_mask`` (they carry the same window,
     model_fast.py:2546-2550). ``q_lens``/``k_lens`` are ignored with the reference's
     warning (attention.py:1128-1132); masked cross-attention is ``cross_attention``.
-    Output: ``[B, Lq, N, D]`` in ``dtype`` (bf16 by default)."""
+    The kernels compute in bf16, so ``dtype`` must be ``torch.bfloat16`` (the reference
+    computes in ``dtype``; any other value raises). Output: bf16 ``[B, Lq, N, D]``."""
+    _check_dtype(dtype)
     if causal:
         raise NotImplementedError("causal masking is not part of this path (the chunked "
                                   "cache carries causality; attention.py:360-365)")
@@ -187,7 +203,7 @@ def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=Non
         lo, hi = window_from_mask(attn_mask, k.shape[1])
     out = attention_segments(q, [(k, v)], kv_lo=lo, kv_hi=hi, softmax_scale=softmax_scale,
                              cross=bool(is_cross_attn) and k.shape[1] <= 4096)
-    return out if dtype == torch.bfloat16 else out.to(dtype)
+    return out
 
 
 flash_attention = attention
@@ -200,11 +216,12 @@ def exact_attention(q, k, v, dtype=torch.bfloat16):
 
 def exact_attention_chunks(q, k_chunks, v_chunks, dtype=torch.bfloat16):
     """attention.py:1048-1058: attention over the concatenation of KV chunks, read in
-    place as segments (no torch.cat, no padding copy). Chunks are ``[B, L_c, N, D]``."""
+    place as segments (no torch.cat, no padding copy). Chunks are ``[B, L_c, N, D]``.
+    ``dtype`` must be bf16, as for :func:`attention`."""
+    _check_dtype(dtype)
     if len(k_chunks) != len(v_chunks):
         raise ValueError("k_chunks and v_chunks differ in length")
-    out = attention_segments(q, list(zip(k_chunks, v_chunks)))
-    return out if dtype == torch.bfloat16 else out.to(dtype)
+    return attention_segments(q, list(zip(k_chunks, v_chunks)))
 
 
 def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16, n_distinct=None):
@@ -212,11 +229,12 @@ def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16, n_distinct=None)
     optional per-batch valid length ``k_lens`` masked (the reference attends all rows;
     ``k_lens=None`` reproduces that). ``n_distinct`` selects the exact deduplicated form of
     attention.py:493-554: rows ``n_distinct..`` of k/v are identical (the context's padding)
-    and are attended as one key weighted by their count (see ``padding_start``)."""
+    and are attended as one key weighted by their count (see ``padding_start``).
+    ``dtype`` must be bf16, as for :func:`attention`."""
+    _check_dtype(dtype)
     if n_distinct is not None and k_lens is not None:
         raise ValueError("dedup reproduces the unmasked attention: pass k_lens or n_distinct")
-    out = attention_segments(q, [(k, v)], k_lens=k_lens, cross=True, n_distinct=n_distinct)
-    return out if dtype == torch.bfloat16 else out.to(dtype)
+    return attention_segments(q, [(k, v)], k_lens=k_lens, cross=True, n_distinct=n_distinct)
 
 
 def padding_start(k: torch.Tensor, v: torch.Tensor) -> int:

@@ -70,9 +70,10 @@ def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softma
         out = torch.empty(q.shape, dtype=torch.bfloat16, device=device)
     p = _params(q, out, segs, kv_lo, kv_hi, None, softmax_scale, num_splits)
     with torch.cuda.device(device):
-        ws_bytes = lib.lbw_attention_workspace_size(ctypes_ref(p))
-        ws = _workspace(device, ws_bytes) if ws_bytes else None
+        stream = _lib.stream_ptr(device)
+        ws_bytes = lib.lbw_attention_fp8kv_workspace_size(ctypes_ref(p))
+        ws = _workspace(device, stream, ws_bytes) if ws_bytes else None
         _lib.check(lib.lbw_attention_fwd_fp8kv(ctypes_ref(p), ws.data_ptr() if ws is not None else None,
-                                               ws_bytes, _lib.stream_ptr(device)),
+                                               ws_bytes, stream),
                    "lbw_attention_fwd_fp8kv")
     return out

@@ -17,7 +17,7 @@ __all__ = [
     "attention_brute_f64", "merge_partials", "window_mask", "num_chunks", "chunk_routing",
     "ordered_chunks", "flat_cache_write_plan", "fp8_e4m3_encode", "fp8_e4m3_decode",
     "quantize_kv_fp8", "dequantize_kv_fp8", "self_attention_layer_ref", "cross_kv_ref",
-    "attn_flops", "cosine", "cross_dedup_bias", "attention_key_bias_ref",
+    "cross_dedup_bias", "attention_key_bias_ref",
 ]
 
 # wan/modules/model.py:44 -- rows of the RoPE frequency tables (frame axis bound).
@@ -290,17 +290,6 @@ def merge_partials(parts):
     for l_, o in zip(lam[1:], outs[1:]):
         out = out + l_.unsqueeze(-1) * o
     return out.permute(0, 2, 1, 3).contiguous()
-
-
-def attn_flops(lq: int, lk: int, heads: int, head_dim: int = 128, batch: int = 1) -> float:
-    """4 * Lq * Lk * D * H: QK^T plus PV at 2 FLOP per multiply-add; softmax excluded."""
-    return 4.0 * lq * lk * head_dim * heads * batch
-
-
-def cosine(a: torch.Tensor, b: torch.Tensor) -> float:
-    a = a.double().flatten()
-    b = b.double().flatten()
-    return float((a @ b) / (a.norm() * b.norm()))
 
 
 # ----------------------------------------------------------------------------- KV caches

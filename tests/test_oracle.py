@@ -288,6 +288,27 @@ def test_chunk_routing_reference_table():
     assert O.num_chunks(-1, 3) == 0 and O.chunk_routing(7, 1) == (0, ())
 
 
+@pytest.mark.parametrize("n", [2, 3, 4, 6])
+def test_ordered_chunks_sink_first_destination_last(n):
+    """chunked_kv_cache.py:47-76, 172-177: simulate the chunked cache writing chunk i (its
+    token ids) into the routed slot; the ordered buffers the attention then reads must be
+    the sink chunk 0 first (once one more chunk exists), the chunk just written last (the
+    destination: the entry the write goes to), and exactly the sink plus the most recent
+    n - 1 chunks, each once. A destination placed first, a reversed leading order or a
+    missing slot fails one of these."""
+    slots = [None] * n
+    for i in range(4 * n + 3):
+        dest, lead = O.chunk_routing(i, n)
+        slots[dest] = i
+        order = O.ordered_chunks(slots, dest, lead)
+        assert order[-1] == i
+        if i >= 1:
+            assert order[0] == 0
+        recent = list(range(max(1, i - (n - 2)), i + 1)) if i >= 1 else [0]
+        want = sorted(set([0] + recent))
+        assert sorted(order) == want and len(order) == len(want)
+
+
 def test_flat_cache_plan_keeps_sink_and_recent_window():
     """Simulate the windowed flat cache over many chunks with token ids: the sink frames
     stay at the front, the rest of the window holds the most recent tokens in order."""
