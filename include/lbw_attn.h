@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define LBW_ABI_VERSION 1
+#define LBW_ABI_VERSION 2
 #define LBW_MAX_KV_SEGMENTS 8
 #define LBW_FP8_BLOCK 64
 
@@ -66,7 +66,8 @@ typedef struct lbw_attn_params {
   int32_t batch, heads, head_dim, lq;
   const void* q;        /* bf16 [B, Lq, H, D] */
   int64_t q_stride_b, q_stride_l, q_stride_h;
-  void* out;            /* bf16 [B, Lq, H, D]; may be NULL when partials are requested */
+  void* out;            /* bf16 (or fp32, see out_dtype) [B, Lq, H, D]; may be NULL when
+                         * partials are requested */
   int64_t o_stride_b, o_stride_l, o_stride_h;
   int32_t n_segments;
   lbw_kv_segment seg[LBW_MAX_KV_SEGMENTS];
@@ -82,7 +83,13 @@ typedef struct lbw_attn_params {
   float* part_o;
   float* part_m;
   float* part_l;
+  /* LBW_OUT_BF16 (0): `out` is bf16. LBW_OUT_FP32 (1): `out` is fp32 [B, Lq, H, D] (16-byte
+   * aligned, strides multiples of 4), the normalised O / l before any bf16 rounding: a check
+   * of the kernels' own arithmetic apart from the output rounding (same kernels, same plan). */
+  int32_t out_dtype;
 } lbw_attn_params;
+#define LBW_OUT_BF16 0
+#define LBW_OUT_FP32 1
 
 /* Bytes of workspace lbw_attention_fwd needs for these params: the split-KV partials (when
  * the call is split) and 256 bytes of work-queue counters, which let the XCDs of the GPU share

@@ -27,6 +27,7 @@ struct AttnKernelArgs {
   uint16_t* out;
   int64_t osb, osl, osh;
   int o16;            // out and its strides allow 16-byte stores
+  int o32;            // out is fp32 (16-byte aligned, strides multiples of 4) instead of bf16
   int nseg;
   SegDesc seg[LBW_MAX_SEGS];
   int64_t total;      // keys in the concatenation
@@ -53,8 +54,9 @@ struct MergeKernelArgs {
   const float* m[16];
   const float* l[16];
   int B, H, Lq, D;
-  uint16_t* out;
+  uint16_t* out;      // bf16, or fp32 when o32
   int64_t osb, osl, osh;
+  int o32;
 };
 
 int attn_lds_bytes();

@@ -707,7 +707,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   // (l32, hl) holds d = 32db + 8g + 4hl .. +3 of row l32).
   unsigned char* stg = lds + 8192 * wave;
   const int rrow = lane >> 4, rch = lane & 15;  // read side: row in a 4-row group, chunk
-  if (a.mode == kModeNormalized) {
+  if (a.mode == kModeNormalized && !a.o32) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -734,11 +734,15 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
     }
   } else {
+    // fp32 rows: the normalised output of an fp32-output call, or the partials.
     // cte_partial contract (TRACK): O and l relative to the true row max, m in scaled units;
     // the split-KV partials for lbw's own merge keep the exponent reference instead.
+    const bool norm32 = a.mode == kModeNormalized;
     float f = 1.0f;
     float m_out = -INFINITY;
-    if (l_tot > 0.0f) {
+    if (norm32) {
+      f = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    } else if (l_tot > 0.0f) {
       if constexpr (TRACK) {
         f = fast_exp2((m_used - m_true) * c);
         m_out = m_true * a.scale;
@@ -750,10 +754,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     }
     const int64_t row0 = ((int64_t)(split * a.B + b) * a.H + h) * a.Lq;
     const int q = q0 + l32;
-    if (q < a.Lq && hl == 0) {
+    if (!norm32 && q < a.Lq && hl == 0) {
       a.part_m[row0 + q] = m_out;
       a.part_l[row0 + q] = l_tot * f;
     }
+    float* const out32 = reinterpret_cast<float*>(a.out) + a.osb * b + a.osh * h;
     // fp32 O in two halves of 64 d (256 B per row each)
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
@@ -775,8 +780,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         const int r = 4 * k + rrow;
         const floatx4 v = *reinterpret_cast<const floatx4*>(stg + r * 256 + ((rch ^ (r & 15)) << 4));
         const int qq = q0 + r;
-        if (qq < a.Lq)
-          *reinterpret_cast<floatx4*>(a.part_o + (row0 + qq) * D + 64 * half + 4 * rch) = v;
+        if (qq < a.Lq) {
+          float* dst = norm32 ? out32 + a.osl * (int64_t)qq : a.part_o + (row0 + qq) * D;
+          *reinterpret_cast<floatx4*>(dst + 64 * half + 4 * rch) = v;
+        }
       }
     }
   }

@@ -2,9 +2,10 @@
 // wan/modules/attention.py:963-990: given per split s the unnormalised O_s (relative to the
 // split's row max), the row max m_s (scaled scores) and the row sum l_s,
 //   out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s,  M = max_s m_s,
-// written as bf16; a row whose every split is empty (all m_s = -inf) yields 0.
+// written as bf16 (fp32 for an fp32-output call); a row whose every split is empty (all m_s =
+// -inf) yields 0.
 //
-// HBM-bound: per (b, h, q) row it reads n * (D + 2) fp32 values and writes D bf16 values.
+// HBM-bound: per (b, h, q) row it reads n * (D + 2) fp32 values and writes D output values.
 // One thread per (row, 4 consecutive d), so every load and store is a 16 / 8-byte vector. The
 // split count is a template parameter, so that a thread issues all of its 3 n loads before it
 // waits for any of them (with a runtime count the loops kept one round trip per load in flight).
@@ -13,7 +14,7 @@
 
 namespace lbw {
 
-template <int N>
+template <int N, bool O32>
 __global__ void __launch_bounds__(256)
 attn_merge_kernel(const MergeKernelArgs a) {
   const int64_t total = (int64_t)a.B * a.H * a.Lq * (a.D / 4);
@@ -47,11 +48,15 @@ attn_merge_kernel(const MergeKernelArgs a) {
       }
     }
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)q + a.osh * h + 4 * dq;
-    u32x2 w;
-    w[0] = pack_bf16x2(num[0] * inv, num[1] * inv);
-    w[1] = pack_bf16x2(num[2] * inv, num[3] * inv);
-    *reinterpret_cast<u32x2*>(op) = w;
+    const int64_t off = a.osb * b + a.osl * (int64_t)q + a.osh * h + 4 * dq;
+    if constexpr (O32) {
+      *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(a.out) + off) = num * inv;
+    } else {
+      u32x2 w;
+      w[0] = pack_bf16x2(num[0] * inv, num[1] * inv);
+      w[1] = pack_bf16x2(num[2] * inv, num[3] * inv);
+      *reinterpret_cast<u32x2*>(a.out + off) = w;
+    }
   }
 }
 
@@ -59,32 +64,30 @@ attn_merge_kernel(const MergeKernelArgs a) {
 int attn_block_m() { return 256; }
 int attn_block_n() { return BN; }
 
+template <bool O32>
+static hipError_t launch_merge_n(const MergeKernelArgs& a, dim3 grid, dim3 block,
+                                 hipStream_t stream) {
+  switch (a.n) {
+#define LBW_MERGE_CASE(n) \
+    case n: hipLaunchKernelGGL((attn_merge_kernel<n, O32>), grid, block, 0, stream, a); break;
+    LBW_MERGE_CASE(1) LBW_MERGE_CASE(2) LBW_MERGE_CASE(3) LBW_MERGE_CASE(4)
+    LBW_MERGE_CASE(5) LBW_MERGE_CASE(6) LBW_MERGE_CASE(7) LBW_MERGE_CASE(8)
+    LBW_MERGE_CASE(9) LBW_MERGE_CASE(10) LBW_MERGE_CASE(11) LBW_MERGE_CASE(12)
+    LBW_MERGE_CASE(13) LBW_MERGE_CASE(14) LBW_MERGE_CASE(15) LBW_MERGE_CASE(16)
+#undef LBW_MERGE_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_attn_merge(const MergeKernelArgs& a, hipStream_t stream) {
   const int64_t total = (int64_t)a.B * a.H * a.Lq * (a.D / 4);
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (blocks < 1) blocks = 1;
   const dim3 grid((uint32_t)blocks), block(256);
-  switch (a.n) {
-    case 1: hipLaunchKernelGGL(attn_merge_kernel<1>, grid, block, 0, stream, a); break;
-    case 2: hipLaunchKernelGGL(attn_merge_kernel<2>, grid, block, 0, stream, a); break;
-    case 3: hipLaunchKernelGGL(attn_merge_kernel<3>, grid, block, 0, stream, a); break;
-    case 4: hipLaunchKernelGGL(attn_merge_kernel<4>, grid, block, 0, stream, a); break;
-    case 5: hipLaunchKernelGGL(attn_merge_kernel<5>, grid, block, 0, stream, a); break;
-    case 6: hipLaunchKernelGGL(attn_merge_kernel<6>, grid, block, 0, stream, a); break;
-    case 7: hipLaunchKernelGGL(attn_merge_kernel<7>, grid, block, 0, stream, a); break;
-    case 8: hipLaunchKernelGGL(attn_merge_kernel<8>, grid, block, 0, stream, a); break;
-    case 9: hipLaunchKernelGGL(attn_merge_kernel<9>, grid, block, 0, stream, a); break;
-    case 10: hipLaunchKernelGGL(attn_merge_kernel<10>, grid, block, 0, stream, a); break;
-    case 11: hipLaunchKernelGGL(attn_merge_kernel<11>, grid, block, 0, stream, a); break;
-    case 12: hipLaunchKernelGGL(attn_merge_kernel<12>, grid, block, 0, stream, a); break;
-    case 13: hipLaunchKernelGGL(attn_merge_kernel<13>, grid, block, 0, stream, a); break;
-    case 14: hipLaunchKernelGGL(attn_merge_kernel<14>, grid, block, 0, stream, a); break;
-    case 15: hipLaunchKernelGGL(attn_merge_kernel<15>, grid, block, 0, stream, a); break;
-    case 16: hipLaunchKernelGGL(attn_merge_kernel<16>, grid, block, 0, stream, a); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  return a.o32 ? launch_merge_n<true>(a, grid, block, stream)
+               : launch_merge_n<false>(a, grid, block, stream);
 }
 
 }  // namespace lbw

@@ -140,9 +140,13 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   if (partials && (p->part_o == nullptr || p->part_m == nullptr || p->part_l == nullptr))
     return fail(LBW_ERR_INVALID, "part_o, part_m and part_l must be given together");
   if (partials && !aligned16(p->part_o)) return fail(LBW_ERR_INVALID, "part_o must be 16-byte aligned");
+  if (p->out_dtype != LBW_OUT_BF16 && p->out_dtype != LBW_OUT_FP32)
+    return fail(LBW_ERR_INVALID, "out_dtype %d: LBW_OUT_BF16 or LBW_OUT_FP32", p->out_dtype);
+  const bool o32 = p->out_dtype == LBW_OUT_FP32;
   if (!partials) {
-    if (p->lq > 0 && (p->out == nullptr || (reinterpret_cast<uintptr_t>(p->out) & 7u) != 0))
-      return fail(LBW_ERR_INVALID, "out must be an 8-byte aligned device pointer");
+    const uintptr_t amask = o32 ? 15u : 7u;
+    if (p->lq > 0 && (p->out == nullptr || (reinterpret_cast<uintptr_t>(p->out) & amask) != 0))
+      return fail(LBW_ERR_INVALID, "out must be a %d-byte aligned device pointer", (int)amask + 1);
     if ((p->o_stride_b & 3) || (p->o_stride_l & 3) || (p->o_stride_h & 3))
       return fail(LBW_ERR_INVALID, "out strides must be multiples of 4 elements");
   }
@@ -157,6 +161,7 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   a.out = static_cast<uint16_t*>(p->out);
   a.osb = p->o_stride_b; a.osl = p->o_stride_l; a.osh = p->o_stride_h;
   a.o16 = aligned16(p->out) && mult8(p->o_stride_b) && mult8(p->o_stride_l) && mult8(p->o_stride_h);
+  a.o32 = o32 ? 1 : 0;
   a.nseg = p->n_segments;
   int64_t start = 0;
   for (int i = 0; i < p->n_segments; ++i) {
@@ -267,6 +272,7 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
     m.B = a.B; m.H = a.H; m.Lq = a.Lq; m.D = p->head_dim;
     m.out = static_cast<uint16_t*>(p->out);
     m.osb = p->o_stride_b; m.osl = p->o_stride_l; m.osh = p->o_stride_h;
+    m.o32 = a.o32;
     e = launch_attn_merge(m, st);
     if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
   }

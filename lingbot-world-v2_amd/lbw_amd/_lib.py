@@ -15,7 +15,10 @@ LIB_PATH = os.path.join(_HERE, "liblbw_attn.so")
 
 MAX_KV_SEGMENTS = 8
 FP8_BLOCK = 64
-ABI_VERSION = 1
+ABI_VERSION = 2
+
+OUT_BF16 = 0
+OUT_FP32 = 1
 
 LBW_OK = 0
 _ERR_NAMES = {1: "invalid argument", 2: "unsupported", 3: "HIP error", 4: "workspace"}
@@ -45,6 +48,7 @@ class AttnParams(ctypes.Structure):
         ("softmax_scale", ctypes.c_float),
         ("num_splits", ctypes.c_int32),
         ("part_o", ctypes.c_void_p), ("part_m", ctypes.c_void_p), ("part_l", ctypes.c_void_p),
+        ("out_dtype", ctypes.c_int32),
     ]
 
 
@@ -72,7 +76,8 @@ EXPORTS = (
     "lbw_attention_workspace_size", "lbw_attention_fp8kv_workspace_size", "lbw_attention_fwd",
     "lbw_cross_attention_fwd",
     "lbw_cross_attention_dedup_fwd",
-    "lbw_attention_fwd_fp8kv", "lbw_attn_merge", "lbw_qk_norm_rope", "lbw_kv_quant_fp8",
+    "lbw_attention_fwd_fp8kv", "lbw_attn_merge", "lbw_qk_norm_rope",
+    "lbw_kv_quant_fp8",
     "lbw_last_error", "lbw_abi_version",
 )
 

@@ -82,6 +82,7 @@ def _fill_segment(seg: _lib.KvSegment, k: torch.Tensor, v: torch.Tensor, k_scale
 
 def _params(q, out, segments, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, parts=None):
     p = _lib.AttnParams()
+    p.out_dtype = _lib.OUT_FP32 if out is not None and out.dtype == torch.float32 else _lib.OUT_BF16
     B, Lq, H, D = q.shape
     p.batch, p.heads, p.head_dim, p.lq = B, H, D, Lq
     p.q = q.data_ptr()
@@ -107,7 +108,8 @@ def _params(q, out, segments, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, p
 def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi=None,
                        k_lens: torch.Tensor | None = None, softmax_scale=None,
                        num_splits: int = 0, out: torch.Tensor | None = None,
-                       cross: bool = False, n_distinct: int | None = None) -> torch.Tensor:
+                       cross: bool = False, n_distinct: int | None = None,
+                       out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """softmax(scale Q K^T) V over the windowed concatenation of KV ``segments``.
 
     q ``[B, Lq, N, 128]``; each segment is ``(k, v)`` with k/v ``[B, L_i, N, 128]`` (strided
@@ -115,7 +117,9 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     indexes the concatenation. ``k_lens`` (int32 ``[B]`` on the device) limits each batch's
     keys. With ``cross``, a single short segment; ``n_distinct`` (cross only) declares keys
     ``n_distinct..`` identical rows, attended as one key of that multiplicity (exact).
-    Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given)."""
+    Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given). ``out_dtype=torch.float32``
+    (or an fp32 ``out``) returns the normalised output before its bf16 rounding, from the same
+    kernels and plan: a check of the kernels' own arithmetic."""
     lib = _lib.load()
     device = q.device
     _check_4d("q", q, device)
@@ -126,7 +130,11 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
         _check_4d("v", v, device)
         segs.append((_as_bf16(k), _as_bf16(v)))
     if out is None:
-        out = torch.empty(q.shape, dtype=torch.bfloat16, device=device)
+        if out_dtype not in (torch.bfloat16, torch.float32):
+            raise ValueError(f"out_dtype {out_dtype}: bfloat16 or float32")
+        out = torch.empty(q.shape, dtype=out_dtype, device=device)
+    elif out.dtype not in (torch.bfloat16, torch.float32) or out.shape != q.shape:
+        raise ValueError("out must be a bf16 or fp32 tensor of q's shape")
     if k_lens is not None:
         k_lens = k_lens.to(device=device, dtype=torch.int32).contiguous()
     p = _params(q, out, segs, kv_lo, kv_hi, k_lens, softmax_scale, 1 if cross else num_splits)

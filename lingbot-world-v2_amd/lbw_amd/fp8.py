@@ -49,13 +49,15 @@ def quantize_kv_fp8(x: torch.Tensor, out: Fp8KV | None = None) -> Fp8KV:
 
 
 def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softmax_scale=None,
-                    num_splits: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+                    num_splits: int = 0, out: torch.Tensor | None = None,
+                    out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """Attention of bf16 q ``[B, Lq, N, 128]`` over fp8 segments ``[(Fp8KV k, Fp8KV v), ...]``.
 
     The kernel converts each 64-token tile's codes exactly to bf16 on their way to LDS (every
     e4m3 value is a bf16 value) and runs the bf16 MFMA loop with q unquantised; the K block
     scale folds into the softmax exponent's multiplier and the V block scale into its addend
-    (and out of the row sum)."""
+    (and out of the row sum). ``out_dtype=torch.float32`` returns the output before its bf16
+    rounding."""
     lib = _lib.load()
     device = q.device
     _check_4d("q", q, device)
@@ -67,7 +69,7 @@ def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softma
                 raise ValueError("fp8 segments hold uint8 codes on q's device")
         segs.append((k.codes, v.codes, k.scales, v.scales))
     if out is None:
-        out = torch.empty(q.shape, dtype=torch.bfloat16, device=device)
+        out = torch.empty(q.shape, dtype=out_dtype, device=device)
     p = _params(q, out, segs, kv_lo, kv_hi, None, softmax_scale, num_splits)
     with torch.cuda.device(device):
         stream = _lib.stream_ptr(device)

@@ -17,7 +17,7 @@ __all__ = [
     "attention_brute_f64", "merge_partials", "window_mask", "num_chunks", "chunk_routing",
     "ordered_chunks", "flat_cache_write_plan", "fp8_e4m3_encode", "fp8_e4m3_decode",
     "quantize_kv_fp8", "dequantize_kv_fp8", "self_attention_layer_ref", "cross_kv_ref",
-    "cross_dedup_bias", "attention_key_bias_ref",
+    "cross_dedup_bias", "attention_key_bias_ref", "windowed_layer_sequence_ref",
 ]
 
 # wan/modules/model.py:44 -- rows of the RoPE frequency tables (frame axis bound).
@@ -435,6 +435,53 @@ def self_attention_layer_ref(x, x_cache, wq, bq, wk, bk, wv, bv, wo, bo, gq, gk,
     vv = torch.cat([vc, v], 0)[None]
     o = attention_ref(q[None], kk, vv)
     return o.reshape(1, -1, C) @ wo.float().T + bo.float()
+
+
+def windowed_layer_sequence_ref(xs, wq, bq, wk, bk, wv, bv, wo, bo, gq, gk, *, heads: int,
+                                frame_hw, kv_cache_size: int, sink_tokens: int,
+                                max_attention_size: int, eps: float = 1e-6, freqs=None):
+    """A Wan self-attention layer run over consecutive one-frame chunks ``xs`` (each
+    ``[1, h*w, C]``, chunk i at latent frame i) with the windowed flat KV cache of
+    model_fast.py:2436-2583, fp32 on the CPU: per chunk, q/k/v as in
+    :func:`self_attention_layer_ref` at start frame i; :func:`flat_cache_write_plan` gives the
+    eviction roll (sink kept, the rest shifted left), the slot and the attention window
+    ``[attn_lo, attn_hi)``; out_i = Wo attention(q_i, K[lo:hi], V[lo:hi]) + bo.
+    Returns the list of outputs ``[1, h*w, C]``."""
+    C = xs[0].shape[-1]
+    D = C // heads
+    freqs = wan_rope_freqs(D) if freqs is None else freqs
+    h, w = frame_hw
+
+    def proj(t, wt, b):
+        return t.float() @ wt.float().T + b.float()
+
+    def qk(t, wt, b, g, sf):
+        y = rms_norm_module(proj(t, wt, b), g.float(), eps)[0]
+        cos, sin = causal_rope_grids(freqs, 1, h, w, start_frame=sf)
+        return rope_apply_rotation(y.view(-1, heads, D), cos, sin)
+
+    kc = torch.zeros(kv_cache_size, heads, D)
+    vc = torch.zeros(kv_cache_size, heads, D)
+    g_end = l_end = 0
+    outs = []
+    for i, x in enumerate(xs):
+        n = x.shape[1]
+        plan = flat_cache_write_plan(kv_cache_size, g_end, l_end, i * n, n, sink_tokens,
+                                     max_attention_size)
+        if plan["roll"] is not None:
+            dst, src, ln = plan["roll"]
+            if ln > 0:
+                kc[dst:dst + ln] = kc[src:src + ln].clone()
+                vc[dst:dst + ln] = vc[src:src + ln].clone()
+        s0, e0 = plan["write"]
+        kc[s0:e0] = qk(x, wk, bk, gk, i)
+        vc[s0:e0] = proj(x, wv, bv)[0].view(-1, heads, D)
+        g_end, l_end = plan["global_end"], plan["local_end"]
+        q = qk(x, wq, bq, gq, i)
+        lo, hi = plan["attn_lo"], plan["attn_hi"]
+        o = attention_ref(q[None], kc[None, lo:hi], vc[None, lo:hi])
+        outs.append(o.reshape(1, -1, C) @ wo.float().T + bo.float())
+    return outs
 
 
 def cross_dedup_bias(k, v, kc: int):

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
     for name in _header_functions():
         assert hasattr(lib, name), name
     lib.lbw_abi_version.restype = ctypes.c_int
-    assert lib.lbw_abi_version() == 1
+    assert lib.lbw_abi_version() == 2
 
 
 def _header_struct_fields(name):

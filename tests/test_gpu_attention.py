@@ -221,6 +221,30 @@ def test_errors_are_loud(lib):
         attention_segments(q, [(q, q)])
 
 
+def test_two_streams_get_separate_workspaces(lib):
+    """Two split-KV calls in flight on two streams at once: each stream has its own workspace
+    (work-queue counters and partials), so neither call takes the other's items or overwrites
+    its partials. Both outputs are checked against the oracle."""
+    from lbw_amd import attention_segments
+    from lbw_amd.attention import _ws_cache
+    cases = [_case(1, 700, 3, [3000], seed=s) for s in (31, 32)]
+    dev_in = [(q.to(DEV), ks[0].to(DEV), vs[0].to(DEV)) for q, ks, vs in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    cur = torch.cuda.current_stream()
+    outs = []
+    for st, (q, k, v) in zip(streams, dev_in):
+        st.wait_stream(cur)
+        with torch.cuda.stream(st):
+            outs.append(attention_segments(q, [(k, v)], num_splits=4))
+    for st in streams:
+        cur.wait_stream(st)
+    torch.cuda.synchronize()
+    keys = {key for key in _ws_cache if key[1] in [st.cuda_stream for st in streams]}
+    assert len(keys) == 2
+    for out, (q, ks, vs) in zip(outs, cases):
+        assert_parity(out, O.attention_ref(q, ks[0], vs[0]), "stream")
+
+
 def _full_size_subset(H, Lq, lk_cache, lk_chunk, heads, rows, seed):
     from lbw_amd import attention_segments
     g = torch.Generator(device=DEV).manual_seed(seed)
@@ -250,6 +274,11 @@ def test_full_size_wan13b_480p_chunk(lib):
 def test_full_size_wan14b_720p_chunk(lib):
     """14B 720p: 1-frame chunk (3600 q) over 12 cached frames + chunk (46800 keys), 40 heads."""
     _full_size_subset(40, 3600, 43200, 3600, heads=[0, 19, 39], rows=256, seed=2)
+
+
+def test_full_size_wan14b_480p_chunk(lib):
+    """14B 480p: 3-frame chunk (4680 q) over 18 cached frames + chunk (32760 keys), 40 heads."""
+    _full_size_subset(40, 4680, 28080, 4680, heads=[0, 21, 39], rows=256, seed=3)
 
 
 def test_cross_attention_dedup_matches_full_context():

@@ -1,0 +1,153 @@
+"""GPU parity of the chunk step at the full benchmark shapes, through the exact pipeline the
+benchmark and the Wan layers run: the fused q/k RMSNorm + 3-D RoPE kernel writes q pre-scaled by
+log2(e)/sqrt(128) and commits the chunk's roped K and its V into their cache slot, then the
+folded-softmax attention kernel (softmax scale ln 2) runs over the whole cache with the host's
+own split choice and its work queues.
+
+Checked against the oracle run from the same bf16 inputs: the qk_post rounding sequence
+(O.qk_post_norm_rope, q with out_scale) and exact fp32 attention (O.attention_ref, scale ln 2)
+on sampled query rows -- always including the rows of the last, partly filled q-tile -- of
+heads spread over the head range, to the bf16 bar of every parity test here.
+
+The same call with fp32 output (the normalised O / l before its bf16 rounding, same kernels and
+plan) is held to the bound that the kernel's own arithmetic fixes: P enters the PV product as
+bf16 (relative rounding <= 2^-9) while the row sum adds the fp32 p, so |o - o_exact| <=
+2^-9 max|V| per head; everything else is fp32. This isolates the kernel from the output
+rounding, and holds for peaked heads too (RMSNorm gains up to 16 on q, where the reference
+moves inside rows), whose |o| near 2-4 no bf16 output can meet 1e-2 for."""
+import math
+
+import pytest
+import torch
+
+import oracle as O
+from parity import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+D = 128
+EPS = 1e-6
+LN2 = math.log(2.0)
+
+
+def _splits_of(q4, segs):
+    """The split count the library plans for this call (from its workspace size)."""
+    import ctypes
+
+    from lbw_amd import _lib
+    from lbw_amd.attention import _params
+    p = _params(q4, q4, segs, None, None, None, LN2, 0)
+    ws = _lib.load().lbw_attention_workspace_size(ctypes.byref(p))
+    B, Lq, H, _ = q4.shape
+    return max(1, (ws - 256) // (B * H * Lq * (D + 2) * 4)) if ws > 256 else 1
+
+
+def _kernel_bound(v_head):
+    """2^-9 max|V| (one bf16 rounding of P), plus fp32 accumulation slack."""
+    return float(v_head.float().abs().max()) * 2.0 ** -9 * 1.01 + 1e-5
+
+
+def _pipeline(H, grid, start_frame, cached, heads, rows, seed, two_segments,
+              gains=(1.0, 2.0, 0.5, 1.5), bf16_bar=True):
+    from lbw_amd import (PRESCALED_SOFTMAX_SCALE, attention_segments, causal_rope_tables,
+                         prescaled_q_scale, qk_norm_rope_, wan_rope_freqs)
+    C = H * D
+    Lq = grid[0] * grid[1] * grid[2]
+    LK = cached + Lq
+    print(f"case H={H} grid={grid} start={start_frame} keys={LK} seed={seed}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    cache_k = torch.randn(1, LK, H, D, generator=g, device=DEV).to(torch.bfloat16)
+    cache_v = torch.randn(1, LK, H, D, generator=g, device=DEV).to(torch.bfloat16)
+    xq = torch.randn(Lq, C, generator=g, device=DEV).to(torch.bfloat16)
+    xk = torch.randn(Lq, C, generator=g, device=DEV).to(torch.bfloat16)
+    xv = torch.randn(Lq, C, generator=g, device=DEV).to(torch.bfloat16)
+    gain = torch.tensor(gains, device=DEV)[torch.arange(H, device=DEV) % len(gains)]
+    wq = ((1 + 0.1 * torch.randn(H, D, generator=g, device=DEV)) * gain[:, None]).reshape(C)
+    wq = wq.to(torch.bfloat16)
+    wk = (1 + 0.1 * torch.randn(C, generator=g, device=DEV)).to(torch.bfloat16)
+    qs = prescaled_q_scale(D)
+
+    tabs = causal_rope_tables(wan_rope_freqs(D), grid, start_frame, device=DEV)
+    q = torch.empty(Lq, C, dtype=torch.bfloat16, device=DEV)
+    cached_k = cache_k[:, :cached].cpu()
+    cached_v = cache_v[:, :cached].cpu()
+    qk_norm_rope_(xq, xk, None, None, wq, wk, tabs, EPS, H, q_out=q,
+                  k_out=cache_k[0, cached:].view(Lq, C), v=xv,
+                  v_out=cache_v[0, cached:].view(Lq, C), q_scale=qs)
+    if two_segments:
+        segs = [(cache_k[:, :cached], cache_v[:, :cached]), (cache_k[:, cached:], cache_v[:, cached:])]
+    else:
+        segs = [(cache_k, cache_v)]
+    q4 = q.view(1, Lq, H, D)
+    out = attention_segments(q4, segs, softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    out32 = attention_segments(q4, segs, softmax_scale=PRESCALED_SOFTMAX_SCALE,
+                               out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    splits = _splits_of(q4, segs)
+    print(f"  planned KV splits: {splits}", flush=True)
+    assert bool(torch.isfinite(out.float()).all())
+
+    # oracle from the same bf16 inputs
+    cos, sin = O.causal_rope_grids(O.wan_rope_freqs(D), *grid, start_frame=start_frame)
+    rq = O.qk_post_norm_rope(xq.cpu(), None, wq.cpu(), cos, sin, out_scale=qs).view(1, Lq, H, D)
+    rk = O.qk_post_norm_rope(xk.cpu(), None, wk.cpu(), cos, sin).view(1, Lq, H, D)
+    # the KV commit: V copied bit for bit, K within one bf16 ulp of the qk_post sequence
+    assert torch.equal(cache_v[0, cached:].cpu(), xv.cpu().view(Lq, H, D))
+    dk = (cache_k[:, cached:].cpu().float() - rk.float()).abs()
+    ulp = rk.float().abs().clamp_min(1e-30) * 2.0 ** -7
+    assert float((dk <= ulp).float().mean()) >= 0.999
+
+    tail0 = (Lq // 256) * 256
+    pick = torch.randperm(tail0, generator=torch.Generator().manual_seed(seed))[:rows]
+    sel = torch.cat([pick, torch.arange(tail0, Lq)]).unique().sort().values
+    out_c = out[:, sel].cpu()
+    out32_c = out32[:, sel].cpu()
+    q_gpu = q4[:, sel].cpu()
+    k_gpu = cache_k[:, cached:].cpu()
+    for h in heads:
+        v = torch.cat([cached_v[:, :, h:h + 1], xv.cpu().view(1, Lq, H, D)[:, :, h:h + 1]], 1)
+        if bf16_bar:
+            # the pipeline against the oracle's own q/k post-processing
+            k = torch.cat([cached_k[:, :, h:h + 1], rk[:, :, h:h + 1]], 1)
+            ref = O.attention_ref(rq[:, sel][:, :, h:h + 1], k, v, softmax_scale=LN2)
+            m = assert_parity(out_c[:, :, h:h + 1], ref, f"head {h}")
+            print(f"  head {h} (gain {float(gain[h]):g}) bf16: {m}", flush=True)
+        # the attention kernel's arithmetic: fp32 output against the oracle on the same q and K
+        k = torch.cat([cached_k[:, :, h:h + 1], k_gpu[:, :, h:h + 1]], 1)
+        ref = O.attention_ref(q_gpu[:, :, h:h + 1], k, v, softmax_scale=LN2)
+        err = float((out32_c[:, :, h:h + 1] - ref).abs().max())
+        bound = _kernel_bound(v)
+        print(f"  head {h} (gain {float(gain[h]):g}) fp32 out: max_abs {err:.3e} "
+              f"(bound {bound:.3e}), max|o| {float(ref.abs().max()):.3f}", flush=True)
+        assert bool(torch.isfinite(out32_c).all()) and err <= bound, (h, err, bound)
+        # the bf16 output is the fp32 one rounded once
+        assert torch.equal(out32_c[:, :, h:h + 1].to(torch.bfloat16), out_c[:, :, h:h + 1])
+    return splits
+
+
+def test_wan14b_720p_chunk_step_pipeline(lib):
+    """The benchmarked step at full size: 14B 720p, 1-frame chunk (45 x 80 = 3600 q, start
+    frame 12) over 12 cached frames + the chunk (46800 keys), 40 heads, one flat cache."""
+    splits = _pipeline(40, (1, 45, 80), 12, 43200, heads=[0, 13, 22, 39], rows=256, seed=5,
+                       two_segments=False)
+    assert splits >= 2    # the split-KV path (partials, queues, merge) is what was checked
+
+
+def test_wan14b_720p_peaked_heads_kernel_arithmetic(lib):
+    """The 14B 720p step with strongly peaked heads (q RMSNorm gains 4, 8, 16): checked on the
+    fp32 output only, against the bound of the kernel's own arithmetic."""
+    _pipeline(40, (1, 45, 80), 12, 43200, heads=[0, 1, 2, 38], rows=256, seed=9,
+              two_segments=False, gains=(4.0, 8.0, 16.0, 1.0), bf16_bar=False)
+
+
+def test_wan14b_480p_chunk_step_pipeline(lib):
+    """14B 480p: 3-frame chunk (3 x 30 x 52 = 4680 q, start frame 18) over 18 cached frames
+    (28080 tokens) + the chunk = 32760 keys, 40 heads; cache and chunk as two segments."""
+    _pipeline(40, (3, 30, 52), 18, 28080, heads=[1, 20, 38], rows=256, seed=6, two_segments=True)
+
+
+def test_wan13b_480p_chunk_step_pipeline(lib):
+    """1.3B 480p: 3-frame chunk (4680 q, start frame 6) over 6 cached frames + the chunk
+    (14040 keys), 12 heads."""
+    _pipeline(12, (3, 30, 52), 6, 9360, heads=[0, 6, 11], rows=256, seed=7, two_segments=False)

@@ -64,6 +64,34 @@ def test_wan13b_layer_over_flat_cache(lib, bias_std, gamma_std):
     _check(out, ref, "layer")
 
 
+@pytest.mark.parametrize("max_att_frames", [5, 4])
+def test_windowed_flat_cache_evicts_with_sink(lib, max_att_frames):
+    """The windowed flat cache past capacity (model_fast.py:2510-2526): 5-frame cache with a
+    1-frame sink, 9 one-frame chunks of 8 x 8 tokens, so the last 4 chunks each roll the
+    cache (everything after the sink moves left by a frame) before their K/V are committed.
+    With a 5-frame attention window the sink is attended; with 4 frames it falls outside.
+    Every chunk's layer output is checked against the oracle's windowed sequence."""
+    from lbw_amd import FlatKVCache, WanSelfAttention
+    g = torch.Generator().manual_seed(8)
+    C, H, F = 512, 4, 64
+    ws = _weights(C, g, 0.02, 0.05)
+    layer = _layer(WanSelfAttention, ws, H)
+    xs = [torch.randn(1, F, C, generator=g).to(torch.bfloat16) for _ in range(9)]
+    cache = FlatKVCache(1, 5 * F, H, 128, device=DEV, sink_tokens=F,
+                        max_attention_size=max_att_frames * F)
+    f = {k: v.float() for k, v in ws.items()}
+    refs = O.windowed_layer_sequence_ref([x.float() for x in xs], f["wq"], f["bq"], f["wk"],
+                                         f["bk"], f["wv"], f["bv"], f["wo"], f["bo"], f["gq"],
+                                         f["gk"], heads=H, frame_hw=(8, 8), kv_cache_size=5 * F,
+                                         sink_tokens=F, max_attention_size=max_att_frames * F)
+    rolls = 0
+    for i, x in enumerate(xs):
+        rolls += cache.plan(i * F, F).roll is not None
+        out = layer.forward(x.to(DEV), (1, 8, 8), i, cache, current_start=i * F)
+        _check(out, refs[i], f"chunk {i} (rolls so far {rolls})")
+    assert rolls == 4
+
+
 def test_chunked_cache_path_equals_flat(lib):
     """The chunked cache (3 slots of one 8 x 8 frame each) gives the flat cache's result: the
     64-token chunks make both layouts walk the same key tiles in the same order."""

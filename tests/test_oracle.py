@@ -408,6 +408,48 @@ def test_layer_ref_shifting_all_frames_changes_nothing():
     assert not torch.allclose(a, c, atol=1e-3)
 
 
+def _seq_weights(C, g):
+    ws = [torch.randn(C, C, generator=g) * 0.1 for _ in range(4)]
+    bs = [torch.randn(C, generator=g) * 0.1 for _ in range(4)]
+    gq, gk = 1 + 0.1 * torch.randn(C, generator=g), 1 + 0.1 * torch.randn(C, generator=g)
+    return (ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], ws[3], bs[3], gq, gk)
+
+
+def test_windowed_sequence_without_eviction_equals_layer_over_all_frames():
+    """A cache large enough never to evict: chunk i attends frames 0..i, which is the layer
+    reference over the i cached frames (contiguous grid from frame 0) plus the chunk."""
+    g = torch.Generator().manual_seed(24)
+    C, H, hw = 256, 2, (3, 4)
+    xs = [torch.randn(1, 12, C, generator=g) for _ in range(4)]
+    wts = _seq_weights(C, g)
+    outs = O.windowed_layer_sequence_ref(xs, *wts, heads=H, frame_hw=hw, kv_cache_size=48,
+                                         sink_tokens=12, max_attention_size=48)
+    for i in range(1, 4):
+        ref = O.self_attention_layer_ref(xs[i], torch.cat(xs[:i], 1), *wts, heads=H,
+                                         grid=(1, *hw), cache_grid=(i, *hw), start_frame=i,
+                                         cache_start_frame=0)
+        assert torch.allclose(outs[i], ref, atol=2e-5), i
+
+
+def test_windowed_sequence_with_eviction_attends_recent_frames():
+    """Cache of 5 frames with a 1-frame sink and a 4-frame attention window: once the cache
+    rolls, the window [end - 4 frames, end) holds exactly frames i-3..i (the sink sits before
+    it), so chunk i equals the layer reference over frames max(0, i-3)..i-1 plus the chunk.
+    A wrong roll (source, destination or length) puts other frames in the window."""
+    g = torch.Generator().manual_seed(25)
+    C, H, hw, F = 256, 2, (3, 4), 12
+    xs = [torch.randn(1, F, C, generator=g) for _ in range(9)]
+    wts = _seq_weights(C, g)
+    outs = O.windowed_layer_sequence_ref(xs, *wts, heads=H, frame_hw=hw, kv_cache_size=5 * F,
+                                         sink_tokens=F, max_attention_size=4 * F)
+    for i in range(1, 9):
+        f0 = max(0, i - 3)
+        ref = O.self_attention_layer_ref(xs[i], torch.cat(xs[f0:i], 1), *wts, heads=H,
+                                         grid=(1, *hw), cache_grid=(i - f0, *hw),
+                                         start_frame=i, cache_start_frame=f0)
+        assert torch.allclose(outs[i], ref, atol=2e-5), i
+
+
 def test_cross_kv_ref_closed_forms():
     """K = RMSNorm(ctx Wk + bk) is scale invariant (bk = 0) and zero for a zero context;
     V = ctx Wv + bv is affine."""
