@@ -108,6 +108,18 @@ size_t lbw_attention_fp8kv_workspace_size(const lbw_attn_params* p);
 int lbw_attention_fwd(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* lbw_attention_fwd for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc); no counterpart in the reference. Same
+ * params and results, no workspace argument: the work-queue counters and split-KV partials
+ * live in a static device array of LBW_NOALLOC_SCRATCH_BYTES that the library holds on each
+ * GPU it runs on until the process ends. Nothing is allocated or freed. With num_splits = 0
+ * the host's split choice is lowered, when needed, to the most splits whose partials fit;
+ * an explicit num_splits whose partials do not fit fails with LBW_ERR_WORKSPACE. Every call
+ * on one GPU shares that GPU's array, so calls that may overlap on one GPU (e.g. on two
+ * streams) race: serialise them, or use lbw_attention_fwd with a workspace each. */
+#define LBW_NOALLOC_SCRATCH_BYTES (64u << 20)
+int lbw_attention_fwd_noalloc(const lbw_attn_params* p, void* stream);
+
 /* Cross-attention to a short context (one segment of <= 4096 keys, typically 512), with the
  * optional per-batch valid length p->k_lens. Single pass, no workspace. */
 int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream);

@@ -279,6 +279,43 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
   return LBW_OK;
 }
 
+// ---- scratch of lbw_attention_fwd_noalloc
+// The work-queue counters and split partials of that entry point live in this file-scope device
+// array instead of a caller's workspace: each GPU the library runs on holds its own copy, at its
+// own address, until the process ends. In host code `scratch` names a host-side stand-in, not
+// the device memory: host code only ever uses the address hipGetSymbolAddress returns for the
+// current device (noalloc_scratch), never the array's name. Calls that overlap on one GPU share
+// the array and race.
+static __device__ __align__(256) unsigned char scratch[LBW_NOALLOC_SCRATCH_BYTES];
+
+// Device address of the current device's `scratch`, looked up once per device (with that
+// device current); nullptr with the error set when the lookup fails.
+void* noalloc_scratch() {
+  static std::mutex mu;
+  static void* ptrs[64] = {nullptr};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    hip_fail(e, "hipGetDevice");
+    return nullptr;
+  }
+  if (dev < 0 || dev >= 64) {
+    fail(LBW_ERR_UNSUPPORTED, "device %d: the no-alloc entry point serves devices 0..63", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  if (ptrs[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+      return nullptr;
+    }
+    ptrs[dev] = ptr;
+  }
+  return ptrs[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -340,6 +377,27 @@ int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, 
   q.kv_hi = end;
   return run_attention(&q, false, nullptr, 0, stream, n_distinct,
                        (double)(L - n_distinct) / (double)(end - n_distinct));
+}
+
+int lbw_attention_fwd_noalloc(const lbw_attn_params* p, void* stream) {
+  Plan plan;
+  int rc = make_plan(p, false, &plan);
+  if (rc != LBW_OK) return rc;
+  lbw_attn_params q = *p;
+  if (plan.ws_bytes > LBW_NOALLOC_SCRATCH_BYTES) {
+    if (p->num_splits > 0)
+      return fail(LBW_ERR_WORKSPACE,
+                  "num_splits %d needs %zu bytes of scratch; lbw_attention_fwd_noalloc holds %zu "
+                  "(ask for fewer splits, 0 = the most that fit, or use lbw_attention_fwd)",
+                  p->num_splits, plan.ws_bytes, (size_t)LBW_NOALLOC_SCRATCH_BYTES);
+    // the host's choice does not fit: the largest split count whose partials do (1 always does)
+    const size_t per = (size_t)p->batch * p->heads * p->lq * (p->head_dim + 2) * sizeof(float);
+    const size_t room = LBW_NOALLOC_SCRATCH_BYTES - 512;
+    q.num_splits = (int)std::max<size_t>(1, std::min<size_t>(plan.splits - 1, room / per));
+  }
+  void* ws = noalloc_scratch();
+  if (ws == nullptr) return LBW_ERR_HIP;
+  return run_attention(&q, false, ws, LBW_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int lbw_attention_fwd_fp8kv(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,

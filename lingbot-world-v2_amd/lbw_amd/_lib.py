@@ -76,7 +76,7 @@ EXPORTS = (
     "lbw_attention_workspace_size", "lbw_attention_fp8kv_workspace_size", "lbw_attention_fwd",
     "lbw_cross_attention_fwd",
     "lbw_cross_attention_dedup_fwd",
-    "lbw_attention_fwd_fp8kv", "lbw_attn_merge", "lbw_qk_norm_rope",
+    "lbw_attention_fwd_fp8kv", "lbw_attention_fwd_noalloc", "lbw_attn_merge", "lbw_qk_norm_rope",
     "lbw_kv_quant_fp8",
     "lbw_last_error", "lbw_abi_version",
 )
@@ -100,6 +100,8 @@ def _declare(lib):
     lib.lbw_cross_attention_dedup_fwd.restype = ctypes.c_int
     lib.lbw_attention_fwd_fp8kv.argtypes = [P(AttnParams), vp, ctypes.c_size_t, vp]
     lib.lbw_attention_fwd_fp8kv.restype = ctypes.c_int
+    lib.lbw_attention_fwd_noalloc.argtypes = [P(AttnParams), vp]
+    lib.lbw_attention_fwd_noalloc.restype = ctypes.c_int
     lib.lbw_attn_merge.argtypes = [i32, P(vp), P(vp), P(vp), i32, i32, i32, i32, vp, i64, i64,
                                    i64, vp]
     lib.lbw_attn_merge.restype = ctypes.c_int
