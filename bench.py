@@ -100,6 +100,20 @@ def run_layer(L, tabs, ev=None):
         ev[2].record()
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (first /proc/cpuinfo entry) and its logical CPU count."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{name} ({os.cpu_count()} logical CPUs visible)"
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The oracle on the host cores: fp32 attention of the same workload, one head at a time
     until the time budget is used, scaled to TFLOP/s."""
@@ -120,7 +134,7 @@ def cpu_baseline(budget_s: float = 12.0):
     dt = time.perf_counter() - t0
     flops = 4.0 * LQ * LK * D * heads
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "cpu_model": _cpu_model(), "kind": "port",
             "sample": f"oracle fp32 attention, {heads} of {H} heads of one layer "
                       f"({LQ} q x {LK} k x {D}), {dt:.1f} s; "
                       f"ms per 40-layer chunk extrapolated: {dt / heads * H * 40 * 1e3:.0f}"}
@@ -255,6 +269,50 @@ def other_configs(dev):
         "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2),
         "projection_TFLOP": round(fl_proj / 1e12, 4)}
     return out
+
+
+def boundary_costs(dev):
+    """Host cost of the Python -> torch.ops.lbw -> C ABI boundary, without padding the GPU queue:
+    ``host_us`` = host time to issue one call while the GPU is busy with earlier work (what the
+    boundary adds on the CPU), ``eager_us`` = wall time per call of back-to-back calls from an idle
+    GPU to the last one's end (what a caller waiting on each call sees), ``gpu_us`` = GPU time
+    per call. For the c4 chunk attention and the 14B 480p cross-attention (300-row mask)."""
+    import torch
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments, cross_attention
+    g = torch.Generator(device=dev).manual_seed(3)
+    rnd = lambda *s: torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)
+    q = rnd(1, LQ, H, D)
+    kc, vc = rnd(1, LK, H, D), rnd(1, LK, H, D)
+    out = torch.empty_like(q)
+    qx = rnd(1, 4680, 40, D)
+    kx, vx = rnd(1, 512, 40, D), rnd(1, 512, 40, D)
+    kl = torch.tensor([300], dtype=torch.int32, device=dev)
+    calls = {
+        "chunk_attention_wan14b_720p": (lambda: attention_segments(
+            q, [(kc, vc)], out=out, softmax_scale=PRESCALED_SOFTMAX_SCALE), 10),
+        "cross_attention_wan14b_480p_300valid": (lambda: cross_attention(qx, kx, vx, k_lens=kl), 50),
+    }
+    res = {}
+    for name, (fn, n) in calls.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        # host issue time: queue a long spin first, so no call waits on the GPU
+        _gpu_busy(200.0)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        host = (time.perf_counter() - t0) / n * 1e6
+        torch.cuda.synchronize()
+        # eager wall time from an idle GPU
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        eager = (time.perf_counter() - t0) / n * 1e6
+        gpu = _time_ms(fn, iters=n) * 1e3
+        res[name] = {"host_us": round(host, 1), "eager_us": round(eager, 1), "gpu_us": round(gpu, 1)}
+    return res
 
 
 def pmc_workload():
@@ -478,6 +536,7 @@ def main():
         del layers
         torch.cuda.empty_cache()
         res["other_configs"] = other_configs(dev)
+        res["boundary_costs"] = boundary_costs(dev)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(res))

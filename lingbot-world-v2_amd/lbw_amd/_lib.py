@@ -1,8 +1,9 @@
-"""ctypes binding of liblbw_attn.so (the C ABI declared in include/lbw_attn.h).
+"""Loaders of the in-tree libraries: liblbw_attn.so (the C ABI declared in
+include/lbw_attn.h, with a ctypes binding for direct ABI use) and liblbw_torch.so, which
+registers that ABI as the torch op set ``torch.ops.lbw`` that lbw_amd calls.
 
-The library is built in-tree (``make -C lingbot-world-v2_amd/csrc``) and loaded from this
-directory. There is no fallback: if the library is missing or a call fails, a RuntimeError
-says so.
+Both are built in-tree (``make -C lingbot-world-v2_amd/csrc``) and loaded from this directory.
+There is no fallback: if a library is missing or a call fails, a RuntimeError says so.
 """
 from __future__ import annotations
 
@@ -12,6 +13,7 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liblbw_attn.so")
+OPS_PATH = os.path.join(_HERE, "liblbw_torch.so")
 
 MAX_KV_SEGMENTS = 8
 FP8_BLOCK = 64
@@ -136,6 +138,64 @@ def load():
             raise RuntimeError(f"liblbw_attn ABI {lib.lbw_abi_version()} != {ABI_VERSION}")
         _lib = lib
         return lib
+
+
+_ops = None
+
+
+def ops():
+    """``torch.ops.lbw``, loading liblbw_torch.so (and the C ABI library under it) once.
+    Raises RuntimeError when either library is missing."""
+    global _ops
+    if _ops is not None:
+        return _ops
+    load()
+    with _lock:
+        if _ops is None:
+            if not os.path.exists(OPS_PATH):
+                raise RuntimeError(
+                    f"{OPS_PATH} is missing: build it with `make -C lingbot-world-v2_amd/csrc` "
+                    "(or __graft_entry__.build()). The attention path has no CPU fallback.")
+            import torch
+            torch.ops.load_library(OPS_PATH)
+            _ops = torch.ops.lbw
+    return _ops
+
+
+def attn_params(q, out, segments, kv_lo=None, kv_hi=None, k_lens=None, softmax_scale=None,
+                num_splits=0, parts=None) -> AttnParams:
+    """``lbw_attn_params`` for direct calls of the C ABI: q ``[B, Lq, N, D]``, out of q's shape
+    (bf16 or fp32) or None, segments ``[(k, v)]`` or ``[(k, v, k_scale, v_scale)]`` (fp8),
+    optional partial outputs ``(O, m, l)``."""
+    import torch
+    p = AttnParams()
+    B, Lq, H, D = q.shape
+    p.batch, p.heads, p.head_dim, p.lq = B, H, D, Lq
+    p.q = q.data_ptr()
+    p.q_stride_b, p.q_stride_l, p.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    if out is not None:
+        p.out = out.data_ptr()
+        p.o_stride_b, p.o_stride_l, p.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
+        p.out_dtype = OUT_FP32 if out.dtype == torch.float32 else OUT_BF16
+    if not 1 <= len(segments) <= MAX_KV_SEGMENTS:
+        raise ValueError(f"{len(segments)} KV segments: 1..{MAX_KV_SEGMENTS} supported")
+    p.n_segments = len(segments)
+    for i, sg in enumerate(segments):
+        k, v = sg[0], sg[1]
+        seg = p.seg[i]
+        seg.k, seg.v, seg.len = k.data_ptr(), v.data_ptr(), k.shape[1]
+        seg.k_stride_b, seg.k_stride_l, seg.k_stride_h = k.stride(0), k.stride(1), k.stride(2)
+        seg.v_stride_b, seg.v_stride_l, seg.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
+        if len(sg) > 2:
+            seg.k_scale, seg.v_scale = sg[2].data_ptr(), sg[3].data_ptr()
+    p.kv_lo = 0 if kv_lo is None else int(kv_lo)
+    p.kv_hi = -1 if kv_hi is None else int(kv_hi)
+    p.k_lens = k_lens.data_ptr() if k_lens is not None else None
+    p.softmax_scale = 0.0 if softmax_scale is None else float(softmax_scale)
+    p.num_splits = int(num_splits)
+    if parts is not None:
+        p.part_o, p.part_m, p.part_l = (t.data_ptr() for t in parts)
+    return p
 
 
 def check(rc: int, what: str):

@@ -8,7 +8,8 @@ without concatenating them (attention.py:1048-1079), and ``attention_partial`` /
 ``attention_merge`` carry the unnormalised (O, row max, row sum) contract of
 ``cte_partial`` / ``cte_merge`` (attention.py:617-645, 963-990).
 
-Every call runs on the tensors' device on torch's current stream and raises when the
+Every call goes through the torch op set ``torch.ops.lbw`` (liblbw_torch.so, over the C ABI
+of liblbw_attn.so), runs on the tensors' device on torch's current stream, and raises when a
 library is missing or rejects the arguments: there is no CPU or SDPA fallback.
 """
 from __future__ import annotations
@@ -25,24 +26,6 @@ __all__ = ["attention", "flash_attention", "exact_attention", "exact_attention_c
            "cross_attention", "attention_partial", "attention_merge", "attention_chain",
            "attention_segments", "window_from_mask", "PRESCALED_SOFTMAX_SCALE",
            "prescaled_q_scale"]
-
-_ws_cache: dict = {}
-
-
-def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """The scratch buffer (split-KV partials and work-queue counters) of the calls on one
-    stream of one device, grown on demand from torch's caching allocator.
-
-    A workspace may back only one in-flight call: calls on one stream run in order, so one
-    buffer per (device, stream) never serves two kernels at once, while two streams get two
-    buffers. The buffer is allocated with ``stream`` current, so the caching allocator only
-    hands a replaced buffer's memory out again in that stream's order."""
-    key = (device.index, stream)
-    buf = _ws_cache.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _ws_cache[key] = buf
-    return buf
 
 
 def _check_dtype(dtype):
@@ -69,42 +52,6 @@ def _check_4d(name, t, device):
         raise RuntimeError(f"{name} must be a GPU tensor (the path has no CPU implementation)")
 
 
-def _fill_segment(seg: _lib.KvSegment, k: torch.Tensor, v: torch.Tensor, k_scale=None,
-                  v_scale=None):
-    seg.k = k.data_ptr()
-    seg.v = v.data_ptr()
-    seg.len = k.shape[1]
-    seg.k_stride_b, seg.k_stride_l, seg.k_stride_h = k.stride(0), k.stride(1), k.stride(2)
-    seg.v_stride_b, seg.v_stride_l, seg.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
-    seg.k_scale = k_scale.data_ptr() if k_scale is not None else None
-    seg.v_scale = v_scale.data_ptr() if v_scale is not None else None
-
-
-def _params(q, out, segments, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, parts=None):
-    p = _lib.AttnParams()
-    p.out_dtype = _lib.OUT_FP32 if out is not None and out.dtype == torch.float32 else _lib.OUT_BF16
-    B, Lq, H, D = q.shape
-    p.batch, p.heads, p.head_dim, p.lq = B, H, D, Lq
-    p.q = q.data_ptr()
-    p.q_stride_b, p.q_stride_l, p.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
-    if out is not None:
-        p.out = out.data_ptr()
-        p.o_stride_b, p.o_stride_l, p.o_stride_h = out.stride(0), out.stride(1), out.stride(2)
-    if not 1 <= len(segments) <= _lib.MAX_KV_SEGMENTS:
-        raise ValueError(f"{len(segments)} KV segments: 1..{_lib.MAX_KV_SEGMENTS} supported")
-    p.n_segments = len(segments)
-    for i, sg in enumerate(segments):
-        _fill_segment(p.seg[i], *sg)
-    p.kv_lo = 0 if kv_lo is None else int(kv_lo)
-    p.kv_hi = -1 if kv_hi is None else int(kv_hi)
-    p.k_lens = k_lens.data_ptr() if k_lens is not None else None
-    p.softmax_scale = 0.0 if softmax_scale is None else float(softmax_scale)
-    p.num_splits = int(num_splits)
-    if parts is not None:
-        p.part_o, p.part_m, p.part_l = (t.data_ptr() for t in parts)
-    return p
-
-
 def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi=None,
                        k_lens: torch.Tensor | None = None, softmax_scale=None,
                        num_splits: int = 0, out: torch.Tensor | None = None,
@@ -120,42 +67,47 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given). ``out_dtype=torch.float32``
     (or an fp32 ``out``) returns the normalised output before its bf16 rounding, from the same
     kernels and plan: a check of the kernels' own arithmetic."""
-    lib = _lib.load()
+    ops = _lib.ops()
     device = q.device
     _check_4d("q", q, device)
     q = _as_bf16(q)
-    segs = []
-    for k, v in segments:
-        _check_4d("k", k, device)
-        _check_4d("v", v, device)
-        segs.append((_as_bf16(k), _as_bf16(v)))
-    if out is None:
-        if out_dtype not in (torch.bfloat16, torch.float32):
-            raise ValueError(f"out_dtype {out_dtype}: bfloat16 or float32")
-        out = torch.empty(q.shape, dtype=out_dtype, device=device)
-    elif out.dtype not in (torch.bfloat16, torch.float32) or out.shape != q.shape:
-        raise ValueError("out must be a bf16 or fp32 tensor of q's shape")
+    ks, vs = _segments(segments, device)
+    scale = 0.0 if softmax_scale is None else float(softmax_scale)
+    lo = 0 if kv_lo is None else int(kv_lo)
+    hi = -1 if kv_hi is None else int(kv_hi)
+    if out is not None:
+        if out.dtype not in (torch.bfloat16, torch.float32) or out.shape != q.shape:
+            raise ValueError("out must be a bf16 or fp32 tensor of q's shape")
+    elif out_dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"out_dtype {out_dtype}: bfloat16 or float32")
     if k_lens is not None:
         k_lens = k_lens.to(device=device, dtype=torch.int32).contiguous()
-    p = _params(q, out, segs, kv_lo, kv_hi, k_lens, softmax_scale, 1 if cross else num_splits)
-    with torch.cuda.device(device):
-        stream = _lib.stream_ptr(device)
-        if cross and n_distinct is not None:
-            _lib.check(lib.lbw_cross_attention_dedup_fwd(ctypes_ref(p), int(n_distinct), stream),
-                       "lbw_cross_attention_dedup_fwd")
-        elif cross:
-            _lib.check(lib.lbw_cross_attention_fwd(ctypes_ref(p), stream), "lbw_cross_attention_fwd")
-        else:
-            ws_bytes = lib.lbw_attention_workspace_size(ctypes_ref(p))
-            ws = _workspace(device, stream, ws_bytes) if ws_bytes else None
-            _lib.check(lib.lbw_attention_fwd(ctypes_ref(p), ws.data_ptr() if ws is not None else None,
-                                             ws_bytes, stream), "lbw_attention_fwd")
+    if cross:
+        if len(ks) != 1:
+            raise ValueError("cross-attention takes one KV segment")
+        fp32 = (out.dtype if out is not None else out_dtype) == torch.float32
+        res = ops.cross_attention(q, ks[0], vs[0], k_lens,
+                                  -1 if n_distinct is None else int(n_distinct), lo, hi, scale,
+                                  fp32)
+        return res if out is None else out.copy_(res)
+    if out is None:
+        return ops.attention(q, ks, vs, lo, hi, k_lens, scale, int(num_splits),
+                             out_dtype == torch.float32)
+    ops.attention_out(q, ks, vs, lo, hi, k_lens, scale, int(num_splits), out)
     return out
 
 
-def ctypes_ref(p):
-    import ctypes
-    return ctypes.byref(p)
+def _segments(segments, device):
+    """(k list, v list) of bf16 ``[B, L_i, N, D]`` segments on ``device``."""
+    if not 1 <= len(segments) <= _lib.MAX_KV_SEGMENTS:
+        raise ValueError(f"{len(segments)} KV segments: 1..{_lib.MAX_KV_SEGMENTS} supported")
+    ks, vs = [], []
+    for k, v in segments:
+        _check_4d("k", k, device)
+        _check_4d("v", v, device)
+        ks.append(_as_bf16(k))
+        vs.append(_as_bf16(v))
+    return ks, vs
 
 
 def window_from_mask(attn_mask: torch.Tensor, lk: int):
@@ -268,32 +220,24 @@ def attention_partial(q, segments, *, kv_lo=None, kv_hi=None, softmax_scale=None
     Returns ``(O [B, N, Lq, D] fp32, m [B, N, Lq] fp32, l [B, N, Lq] fp32)`` with
     O = exp(s - m) V, m the row max of the scaled scores and l = sum exp(s - m)
     (m = -inf, l = 0 for rows with no keys)."""
-    lib = _lib.load()
+    ops = _lib.ops()
     device = q.device
     _check_4d("q", q, device)
     q = _as_bf16(q)
-    segs = [(_as_bf16(k), _as_bf16(v)) for k, v in segments]
-    B, Lq, H, D = q.shape
-    po = torch.empty(B, H, Lq, D, dtype=torch.float32, device=device)
-    pm = torch.empty(B, H, Lq, dtype=torch.float32, device=device)
-    pl = torch.empty(B, H, Lq, dtype=torch.float32, device=device)
-    p = _params(q, None, segs, kv_lo, kv_hi, None, softmax_scale, 1, parts=(po, pm, pl))
-    with torch.cuda.device(device):
-        _lib.check(lib.lbw_attention_fwd(ctypes_ref(p), None, 0, _lib.stream_ptr(device)),
-                   "lbw_attention_fwd(partials)")
-    return po, pm, pl
+    ks, vs = _segments(segments, device)
+    return ops.attention_partial(q, ks, vs, 0 if kv_lo is None else int(kv_lo),
+                                 -1 if kv_hi is None else int(kv_hi),
+                                 0.0 if softmax_scale is None else float(softmax_scale))
 
 
 def attention_merge(parts, out: torch.Tensor | None = None) -> torch.Tensor:
     """cte_merge (attention.py:963-990): out = sum_c e^(m_c - M) O_c / sum_c e^(m_c - M) l_c
     over partials ``(O [B, N, Lq, D], m [B, N, Lq], l [B, N, Lq])`` -> bf16 ``[B, Lq, N, D]``."""
-    import ctypes
-    lib = _lib.load()
+    ops = _lib.ops()
     if not 1 <= len(parts) <= 16:
         raise ValueError("1..16 partials")
     po0 = parts[0][0]
     B, H, Lq, D = po0.shape
-    device = po0.device
     for o, m, l in parts:
         if o.shape != po0.shape or m.shape != (B, H, Lq) or l.shape != (B, H, Lq):
             raise ValueError("partials differ in shape")
@@ -301,17 +245,10 @@ def attention_merge(parts, out: torch.Tensor | None = None) -> torch.Tensor:
             raise ValueError("partials must be contiguous")
         if o.dtype != torch.float32 or m.dtype != torch.float32 or l.dtype != torch.float32:
             raise ValueError("partials must be float32")
+    os_, ms, ls = [p[0] for p in parts], [p[1] for p in parts], [p[2] for p in parts]
     if out is None:
-        out = torch.empty(B, Lq, H, D, dtype=torch.bfloat16, device=device)
-    n = len(parts)
-    arr = ctypes.c_void_p * n
-    po = arr(*[p[0].data_ptr() for p in parts])
-    pm = arr(*[p[1].data_ptr() for p in parts])
-    pl = arr(*[p[2].data_ptr() for p in parts])
-    with torch.cuda.device(device):
-        _lib.check(lib.lbw_attn_merge(n, po, pm, pl, B, H, Lq, D, out.data_ptr(), out.stride(0),
-                                      out.stride(1), out.stride(2), _lib.stream_ptr(device)),
-                   "lbw_attn_merge")
+        return ops.attention_merge(os_, ms, ls)
+    ops.attention_merge_out(os_, ms, ls, out)
     return out
 
 

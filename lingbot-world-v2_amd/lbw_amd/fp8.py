@@ -13,7 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import _as_bf16, _check_4d, _params, _workspace, ctypes_ref
+from .attention import _as_bf16, _check_4d
 
 __all__ = ["Fp8KV", "quantize_kv_fp8", "attention_fp8kv"]
 
@@ -29,7 +29,7 @@ class Fp8KV:
 
 def quantize_kv_fp8(x: torch.Tensor, out: Fp8KV | None = None) -> Fp8KV:
     """bf16 ``[B, L, N, 128]`` -> :class:`Fp8KV` (into ``out`` when given)."""
-    lib = _lib.load()
+    ops = _lib.ops()
     _check_4d("x", x, x.device)
     x = _as_bf16(x)
     B, L, H, D = x.shape
@@ -41,10 +41,7 @@ def quantize_kv_fp8(x: torch.Tensor, out: Fp8KV | None = None) -> Fp8KV:
         raise ValueError("codes must be contiguous [B, L, N, D] uint8")
     if out.scales.shape != (B, H, nblk) or not out.scales.is_contiguous():
         raise ValueError(f"scales must be contiguous [B, N, {nblk}] fp32")
-    with torch.cuda.device(x.device):
-        _lib.check(lib.lbw_kv_quant_fp8(x.data_ptr(), B, L, H, D, x.stride(0), x.stride(1),
-                                        x.stride(2), out.codes.data_ptr(), out.scales.data_ptr(),
-                                        BLOCK, _lib.stream_ptr(x.device)), "lbw_kv_quant_fp8")
+    ops.kv_quant_fp8_(x, out.codes, out.scales)
     return out
 
 
@@ -58,24 +55,24 @@ def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softma
     scale folds into the softmax exponent's multiplier and the V block scale into its addend
     (and out of the row sum). ``out_dtype=torch.float32`` returns the output before its bf16
     rounding."""
-    lib = _lib.load()
+    ops = _lib.ops()
     device = q.device
     _check_4d("q", q, device)
     q = _as_bf16(q)
-    segs = []
+    if not 1 <= len(segments) <= _lib.MAX_KV_SEGMENTS:
+        raise ValueError(f"{len(segments)} KV segments: 1..{_lib.MAX_KV_SEGMENTS} supported")
+    kc, vc, ksc, vsc = [], [], [], []
     for k, v in segments:
         for t in (k, v):
             if t.codes.dtype != torch.uint8 or t.codes.device != device:
                 raise ValueError("fp8 segments hold uint8 codes on q's device")
-        segs.append((k.codes, v.codes, k.scales, v.scales))
-    if out is None:
-        out = torch.empty(q.shape, dtype=out_dtype, device=device)
-    p = _params(q, out, segs, kv_lo, kv_hi, None, softmax_scale, num_splits)
-    with torch.cuda.device(device):
-        stream = _lib.stream_ptr(device)
-        ws_bytes = lib.lbw_attention_fp8kv_workspace_size(ctypes_ref(p))
-        ws = _workspace(device, stream, ws_bytes) if ws_bytes else None
-        _lib.check(lib.lbw_attention_fwd_fp8kv(ctypes_ref(p), ws.data_ptr() if ws is not None else None,
-                                               ws_bytes, stream),
-                   "lbw_attention_fwd_fp8kv")
-    return out
+        kc.append(k.codes)
+        vc.append(v.codes)
+        ksc.append(k.scales)
+        vsc.append(v.scales)
+    lo = 0 if kv_lo is None else int(kv_lo)
+    hi = -1 if kv_hi is None else int(kv_hi)
+    scale = 0.0 if softmax_scale is None else float(softmax_scale)
+    res = ops.attention_fp8kv(q, kc, vc, ksc, vsc, lo, hi, scale, int(num_splits),
+                              (out.dtype if out is not None else out_dtype) == torch.float32)
+    return res if out is None else out.copy_(res)

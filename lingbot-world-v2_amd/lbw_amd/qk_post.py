@@ -21,7 +21,6 @@ import math
 import torch
 
 from . import _lib
-from .attention import ctypes_ref
 from .rope import RopeTables
 
 __all__ = ["qk_norm_rope", "qk_norm_rope_", "qk_norm_rope3", "qk_norm_rope_t", "qk_norm_rope_t3",
@@ -61,7 +60,7 @@ def qk_norm_rope_(q, k, bq, bk, wq, wk, rope: RopeTables, eps: float, heads: int
     stride 1, e.g. ``cache_kt[:, :, s:e]`` of a ``[H, D, capacity]`` cache.
     ``k=None`` processes q alone (``k_out``/``wk``/``bk`` ignored). Optionally copies v into
     v_out (rows; the new chunk's V commit). ``bq``/``bk`` may be None."""
-    lib = _lib.load()
+    ops = _lib.ops()
     L, C = q.shape
     if layout not in ("rows", "dmajor"):
         raise ValueError(f"layout {layout!r}: 'rows' or 'dmajor'")
@@ -73,44 +72,27 @@ def qk_norm_rope_(q, k, bq, bk, wq, wk, rope: RopeTables, eps: float, heads: int
         if k.shape[0] != L:
             raise ValueError(f"k has {k.shape[0]} rows, q has {L}")
     outs = (("q_out", q_out),) + ((("k_out", k_out),) if has_k else ())
-    strides = []
     for name, t in outs:
         if layout == "rows":
             _rows(name, t, C)
             if t.shape[0] != L:
                 raise ValueError(f"{name} has {t.shape[0]} rows, q has {L}")
-            strides.append(t.stride(0))
         else:
-            strides.append(_dmajor(name, t, heads, D, L))
+            _dmajor(name, t, heads, D, L)
     vecs = (("wq", wq), ("bq", bq)) + ((("wk", wk), ("bk", bk)) if has_k else ())
     for name, t in vecs:
         if t is not None and (t.numel() != C or t.dtype != torch.bfloat16 or not t.is_contiguous()):
             raise ValueError(f"{name} must be a contiguous bf16 [C] vector")
-    p = _lib.QkNormRopeParams()
-    p.tokens, p.dim, p.heads = L, C, heads
-    p.q, p.q_stride = q.data_ptr(), q.stride(0)
-    p.bq = bq.data_ptr() if bq is not None else None
-    p.wq = wq.data_ptr()
-    p.q_out, p.q_out_stride = q_out.data_ptr(), strides[0]
-    if has_k:
-        p.k, p.k_stride = k.data_ptr(), k.stride(0)
-        p.bk = bk.data_ptr() if bk is not None else None
-        p.wk = wk.data_ptr()
-        p.k_out, p.k_out_stride = k_out.data_ptr(), strides[1]
-    p.eps = float(eps)
-    p.rope = rope.packed.data_ptr()
-    p.grid_f, p.grid_h, p.grid_w, p.s0, p.s1 = rope.f, rope.h, rope.w, rope.s0, rope.s1
-    p.q_out_scale, p.k_out_scale = float(q_scale), float(k_scale)
-    p.out_layout = LAYOUT_ROWS if layout == "rows" else LAYOUT_DMAJOR
     if v is not None:
         _rows("v", v, C)
         _rows("v_out", v_out, C)
-        p.v, p.v_stride = v.data_ptr(), v.stride(0)
-        p.v_out, p.v_out_stride = v_out.data_ptr(), v_out.stride(0)
     if rope.packed.device != q.device:
         raise ValueError("rope tables are on another device")
-    with torch.cuda.device(q.device):
-        _lib.check(lib.lbw_qk_norm_rope(ctypes_ref(p), _lib.stream_ptr(q.device)), "lbw_qk_norm_rope")
+    ops.qk_norm_rope_(q, k, bq, bk if has_k else None, wq, wk if has_k else None, rope.packed,
+                      [rope.f, rope.h, rope.w, rope.s0, rope.s1], float(eps), heads, q_out,
+                      k_out if has_k else None, v, v_out if v is not None else None,
+                      float(q_scale), float(k_scale),
+                      LAYOUT_ROWS if layout == "rows" else LAYOUT_DMAJOR)
     return (q_out, k_out) if has_k else q_out
 
 

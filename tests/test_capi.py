@@ -199,3 +199,28 @@ def test_prescaled_pairing_is_exactly_one_in_fp32():
     for d in (64, 128):
         assert math.isclose(prescaled_q_scale(d) * PRESCALED_SOFTMAX_SCALE, 1 / math.sqrt(d),
                             rel_tol=1e-15)
+
+
+def test_torch_op_set_registers_with_shapes():
+    """liblbw_torch.so registers the C ABI as torch.ops.lbw; its Meta kernels give every
+    functional op's output shape and dtype (what tracing under torch.compile needs), with no
+    GPU and no launch."""
+    import torch
+    from lbw_amd import _lib
+    ops = _lib.ops()
+    for name in ("attention", "attention_out", "cross_attention", "attention_fp8kv",
+                 "attention_partial", "attention_merge", "attention_merge_out", "qk_norm_rope_",
+                 "kv_quant_fp8_"):
+        assert hasattr(ops, name), name
+    q = torch.empty(2, 10, 3, 128, dtype=torch.bfloat16, device="meta")
+    k = torch.empty(2, 70, 3, 128, dtype=torch.bfloat16, device="meta")
+    o = ops.attention(q, [k, k], [k, k], 0, -1, None, 0.0, 0, False)
+    assert o.shape == q.shape and o.dtype == torch.bfloat16
+    assert ops.attention(q, [k], [k], 0, -1, None, 0.0, 0, True).dtype == torch.float32
+    assert ops.cross_attention(q, k, k, None, -1, 0, -1, 0.0, False).shape == q.shape
+    po, pm, pl = ops.attention_partial(q, [k], [k], 0, -1, 0.0)
+    assert po.shape == (2, 3, 10, 128) and pm.shape == (2, 3, 10) and pl.dtype == torch.float32
+    assert ops.attention_merge([po, po], [pm, pm], [pl, pl]).shape == q.shape
+    c8 = torch.empty(2, 70, 3, 128, dtype=torch.uint8, device="meta")
+    s8 = torch.empty(2, 3, 2, dtype=torch.float32, device="meta")
+    assert ops.attention_fp8kv(q, [c8], [c8], [s8], [s8], 0, -1, 0.0, 0, False).shape == q.shape

@@ -222,11 +222,11 @@ def test_errors_are_loud(lib):
 
 
 def test_two_streams_get_separate_workspaces(lib):
-    """Two split-KV calls in flight on two streams at once: each stream has its own workspace
-    (work-queue counters and partials), so neither call takes the other's items or overwrites
-    its partials. Both outputs are checked against the oracle."""
+    """Two split-KV calls in flight on two streams at once: each call's workspace (work-queue
+    counters and partials) comes from the caching allocator on its own stream, so neither call
+    takes the other's items or overwrites its partials. Both outputs are checked against the
+    oracle."""
     from lbw_amd import attention_segments
-    from lbw_amd.attention import _ws_cache
     cases = [_case(1, 700, 3, [3000], seed=s) for s in (31, 32)]
     dev_in = [(q.to(DEV), ks[0].to(DEV), vs[0].to(DEV)) for q, ks, vs in cases]
     streams = [torch.cuda.Stream(), torch.cuda.Stream()]
@@ -239,8 +239,6 @@ def test_two_streams_get_separate_workspaces(lib):
     for st in streams:
         cur.wait_stream(st)
     torch.cuda.synchronize()
-    keys = {key for key in _ws_cache if key[1] in [st.cuda_stream for st in streams]}
-    assert len(keys) == 2
     for out, (q, ks, vs) in zip(outs, cases):
         assert_parity(out, O.attention_ref(q, ks[0], vs[0]), "stream")
 

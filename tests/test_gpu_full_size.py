@@ -36,8 +36,7 @@ def _splits_of(q4, segs):
     import ctypes
 
     from lbw_amd import _lib
-    from lbw_amd.attention import _params
-    p = _params(q4, q4, segs, None, None, None, LN2, 0)
+    p = _lib.attn_params(q4, q4, segs, None, None, None, LN2, 0)
     ws = _lib.load().lbw_attention_workspace_size(ctypes.byref(p))
     B, Lq, H, _ = q4.shape
     return max(1, (ws - 256) // (B * H * Lq * (D + 2) * 4)) if ws > 256 else 1

@@ -25,9 +25,8 @@ def _inputs(B, Lq, H, L, seed):
 
 def _noalloc(lib, q, k, v, splits):
     from lbw_amd import _lib
-    from lbw_amd.attention import _params
     out = torch.empty(q.shape, dtype=torch.bfloat16, device=DEV)
-    p = _params(q, out, [(k, v)], None, None, None, None, splits)
+    p = _lib.attn_params(q, out, [(k, v)], None, None, None, None, splits)
     rc = lib.lbw_attention_fwd_noalloc(ctypes.byref(p), _lib.stream_ptr())
     _lib.check(rc, "lbw_attention_fwd_noalloc")
     return out
@@ -53,9 +52,8 @@ def test_noalloc_rejects_splits_beyond_its_scratch(lib):
     """An explicit split count whose partials exceed the scratch fails with a clear error (no
     launch); the host's own choice (num_splits = 0) is lowered to what fits instead."""
     from lbw_amd import _lib
-    from lbw_amd.attention import _params
     q = torch.empty(1, 3600, 40, 128, dtype=torch.bfloat16, device=DEV)
     k = torch.empty(1, 46800, 40, 128, dtype=torch.bfloat16, device=DEV)
-    p = _params(q, q, [(k, k)], None, None, None, None, 3)
+    p = _lib.attn_params(q, q, [(k, k)], None, None, None, None, 3)
     rc = lib.lbw_attention_fwd_noalloc(ctypes.byref(p), _lib.stream_ptr())
     assert rc == 4 and b"scratch" in lib.lbw_last_error()
