@@ -65,6 +65,10 @@ int attn_block_n();
 hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream);
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream);
 hipError_t launch_attn_merge(const MergeKernelArgs& a, hipStream_t stream);
+// Cross-attention (cross_attn.hip): one segment, single pass, persistent workgroups on
+// `num_cus` CUs; keys beyond cross_attn_max_keys_resident() run in chunks.
+hipError_t launch_cross_attn(const AttnKernelArgs& a, int num_cus, hipStream_t stream);
+int cross_attn_max_keys_resident();
 
 struct QkNormRopeArgs {
   int L, C, H;

@@ -16,6 +16,89 @@ constexpr float TAU = 8.0f;  // lazy-rescale threshold, log2 units
 constexpr float M_INIT = -1e30f;  // initial exponent reference (finite stand-in for -inf)
 constexpr float P_LIMIT = 65536.0f;  // largest per-lane row sum before the reference moves
 
+// ---- helpers shared by the attention kernels
+
+// LDS row swizzle of the 256-byte K/V rows: 16-byte chunk c of row r is stored at chunk
+// c ^ swz(r), which makes the K row reads and the V transpose reads conflict-free.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
+
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+
+// LDS reads at an integer LDS byte address, so the constant part of an address folds into the
+// instruction's offset field.
+__device__ __forceinline__ u32x2 lds_read_tr16(int addr) {
+  const shortx4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_shortx4*)(uintptr_t)addr);
+  return __builtin_bit_cast(u32x2, v);
+}
+__device__ __forceinline__ u32x4 lds_read_b128(int addr) {
+  return *(const lds_u32x4*)(uintptr_t)addr;
+}
+
+// 16 bytes per lane HBM -> LDS (global_load_lds_dwordx4): lane l's bytes from sbase + voff land
+// at LDS byte address lds_dst + 16 l. Inline asm rather than the builtin: the compiler's wait
+// insertion treats an in-flight builtin copy as a hazard for every later LDS transpose read and
+// waits for all copies before each one, which would serialise the prefetch. The kernel waits
+// for the tiles it reads itself (wait_tiles_outstanding, then a barrier).
+__device__ __forceinline__ void dma16(const unsigned char* sbase, uint32_t voff, uint32_t lds_dst) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_dst) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)p;
+}
+
+// Materialises a kernel argument in a scalar register at this point. Its scalar load is then
+// waited for here, before the main loop: a scalar load still pending inside the loop (scalar
+// loads complete out of order) turns every LDS wait there into a wait for all LDS reads.
+__device__ __forceinline__ float sreg(float x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+__device__ __forceinline__ int sreg(int x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
+
+// Hides a value from the optimiser (keeps a base register from being re-associated with
+// constant offsets that would no longer fit the 16-bit LDS immediate).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Scores of keys outside the tile's valid rows [tvlo, tvhi) -> -inf (S^T register layout);
+// rows from mrow on get `add` (the log-multiplicity of deduplicated keys).
+// Sign-bit arithmetic on per-lane integers instead of one comparison mask per element: the
+// sixteen 64-bit lane masks would otherwise all be live in scalar registers at once.
+__device__ __forceinline__ void mask_scores(floatx16& sc, int kb, int tvlo, int tvhi, int hl,
+                                            int mrow, float add) {
+  asm volatile("" ::: "memory");
+  const int k0 = 32 * kb + 4 * hl;  // key of register 0 in this lane
+  const int a = k0 - tvlo, bnd = tvhi - 1 - k0, cm = k0 - mrow;
+  const uint32_t addb = __float_as_uint(add);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int o = 8 * (r >> 2) + (r & 3);              // key - k0 of register r
+    const uint32_t out = (uint32_t)(((a + o) | (bnd - o)) >> 31);  // ~0: key outside [tvlo, tvhi)
+    const uint32_t biased = ~(uint32_t)((cm + o) >> 31);           // ~0: key >= mrow
+    const float x = sc[r] + __uint_as_float(addb & biased);
+    sc[r] = __uint_as_float((__float_as_uint(x) & ~out) | (0xff800000u & out));
+  }
+}
+
+__device__ __forceinline__ void scale_acc(floatx16 (&o)[4], float alpha) {
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+}
+
+
+// ---- tile walk
+
 __device__ __forceinline__ int seg_tiles(const SegDesc& s, int64_t lo, int64_t hi, int64_t& la,
                                          int64_t& lb) {
   if (s.len <= 0) return 0;

@@ -232,7 +232,7 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
 }
 
 int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes, void* stream,
-                  int64_t mult_key = -1, double mult = 1.0) {
+                  int64_t mult_key = -1, double mult = 1.0, bool cross = false) {
   Plan plan;
   int rc = make_plan(p, fp8, &plan);
   if (rc != LBW_OK) return rc;
@@ -243,6 +243,22 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
     a.mult_raw = (float)(log(mult) / (double)a.scale);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // Cross-attention: the persistent kernel whenever the keys may fit its LDS-resident chunk
+  // (per-batch k_lens are only known on the device; longer batches run there in chunks). A
+  // context the host knows to be longer goes to the chunk kernel as a single pass, which
+  // streams it faster than the cross kernel's chunk reloads.
+  if (cross && a.k_lens == nullptr && a.hi - a.lo > cross_attn_max_keys_resident()) cross = false;
+  if (cross) {
+    // one segment, single pass: the persistent cross-attention kernel; its chunk loads address
+    // up to 320 rows with 32-bit offsets from the chunk's first row
+    const lbw_kv_segment& s0 = p->seg[0];
+    if (s0.k_stride_l * 2 * cross_attn_max_keys_resident() >= (int64_t(1) << 32) ||
+        s0.v_stride_l * 2 * cross_attn_max_keys_resident() >= (int64_t(1) << 32))
+      return fail(LBW_ERR_UNSUPPORTED, "cross-attention: K/V row stride too large");
+    hipError_t e = launch_cross_attn(a, num_cus(), st);
+    if (e != hipSuccess) return hip_fail(e, "cross-attention kernel launch");
+    return LBW_OK;
+  }
   const bool ws_ok = ws != nullptr && ws_bytes >= plan.ws_bytes && aligned16(ws);
   if (ws_ok) {
     a.queue = reinterpret_cast<uint32_t*>(static_cast<unsigned char*>(ws) + plan.queue_off);
@@ -347,9 +363,11 @@ int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream) {
     return fail(LBW_ERR_INVALID, "cross-attention context of %lld keys exceeds 4096",
                 (long long)p->seg[0].len);
   if (p->num_splits > 1) return fail(LBW_ERR_INVALID, "cross-attention is single pass");
+  if (p->part_o != nullptr || p->part_m != nullptr || p->part_l != nullptr)
+    return fail(LBW_ERR_INVALID, "cross-attention has no partials mode");
   lbw_attn_params q = *p;
   q.num_splits = 1;
-  return run_attention(&q, false, nullptr, 0, stream);
+  return run_attention(&q, false, nullptr, 0, stream, -1, 1.0, true);
 }
 
 int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, void* stream) {
@@ -364,9 +382,11 @@ int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, 
   if (p->k_lens != nullptr || p->kv_lo != 0 || p->kv_hi >= 0)
     return fail(LBW_ERR_INVALID, "dedup attends the whole context: no k_lens or window");
   if (p->num_splits > 1) return fail(LBW_ERR_INVALID, "cross-attention is single pass");
+  if (p->part_o != nullptr || p->part_m != nullptr || p->part_l != nullptr)
+    return fail(LBW_ERR_INVALID, "cross-attention has no partials mode");
   lbw_attn_params q = *p;
   q.num_splits = 1;
-  if (n_distinct == L) return run_attention(&q, false, nullptr, 0, stream);
+  if (n_distinct == L) return run_attention(&q, false, nullptr, 0, stream, -1, 1.0, true);
   // The distinct keys plus the r identical ones up to the end of their 64-key tile (free: the
   // tile is read anyway), each of those weighted m / r (m = L - n_distinct identical rows in
   // all): cross_dedup_bias's log(m / r) form. Spreading the weight over r bf16 probabilities
@@ -376,7 +396,7 @@ int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, 
   q.kv_lo = 0;
   q.kv_hi = end;
   return run_attention(&q, false, nullptr, 0, stream, n_distinct,
-                       (double)(L - n_distinct) / (double)(end - n_distinct));
+                       (double)(L - n_distinct) / (double)(end - n_distinct), true);
 }
 
 int lbw_attention_fwd_noalloc(const lbw_attn_params* p, void* stream) {

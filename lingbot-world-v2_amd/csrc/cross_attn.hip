@@ -1,0 +1,412 @@
+// Cross-attention of the chunk's queries to a short context (gfx950), kernel 3 of the path: the
+// reference's wan_cross_attn (kernels/cross_attention.py:17-123) behind _nki_cross_attention
+// (wan/modules/attention.py:280-311), a single softmax over the (<= 512) context keys.
+//
+// out = softmax(scale Q K^T) V over the keys [lo, hi) of one context segment; hi is limited per
+// batch by k_lens (the masked mode), and for the exact dedup of attention.py:493-554 the keys from
+// mult_key on carry the log of their multiplicity (mult_raw, added to their raw scores).
+//
+// Schedule: persistent workgroups (one per CU, 8 waves). The work is cut into rounds, a round
+// being 256 queries (8 waves x 32) of one (batch, head); workgroup g runs a contiguous range of
+// the rounds, in (batch, head)-major order, and XCD x holds an eighth of the range, so the heads
+// of an XCD share its L2. The K and V rows of the round's (batch, head) -- up to 320 keys -- sit
+// in LDS whole (160 KB: the CU's entire LDS) and stay there across the consecutive rounds of that
+// head: loaded once per head and workgroup, and within a head the waves run their queries with
+// no barrier at all, so one wave's Q loads and output stores overlap the MFMA work of the
+// others. A context longer than 320 keys is processed in 320-key chunks, every round reloading
+// every chunk (a barrier around each load), the per-wave softmax state carrying across chunks.
+//
+// Per wave the arithmetic is the chunk kernel's (attn_fwd_bf16.hip): S^T = K Q^T and
+// O^T = V^T P^T with v_mfma_f32_32x32x16_bf16 (one query per lane column, Q in registers, K rows
+// and V^T fragments from the swizzled LDS rows), an online softmax in base 2 against an exponent
+// reference that moves lazily (a sub-block whose row sum passes 2^16 moves it to the row max and
+// redoes its exponentials; O and l share the reference, so O / l is exact), and the softmax of
+// sub-block j on the VALU overlapping the MFMAs of S_{j+1} and PV_{j-1}.
+
+#include "attn_tiles.h"
+
+namespace lbw {
+namespace {
+
+constexpr int XW = 8;                     // waves per workgroup
+constexpr int XCH = 320;                  // keys resident in LDS per chunk
+constexpr int XSB = XCH / 32;             // 32-key sub-blocks per chunk
+constexpr int XROWB = D * 2;              // bytes per K/V row
+constexpr int XSUBB = 32 * XROWB;         // bytes per sub-block (8 KB)
+constexpr int XV0 = XCH * XROWB;          // V rows follow the K rows (80 KB)
+constexpr int XLDS = 2 * XCH * XROWB;     // 160 KB
+constexpr int XKA = 2, XVA = 2;           // MFMA pairs ahead that K / V fragments are read
+constexpr int XKR = XKA + 2, XVR = XVA + 2;
+static_assert(8 % XKR == 0 && 8 % XVR == 0, "fragment rings must divide 8");
+static_assert(XLDS <= 160 * 1024, "K and V chunks must fit the LDS");
+
+// K sub-block j lies at j * 8 KB, V sub-block j at XV0 + j * 8 KB. An LDS read's immediate offset reaches 64 KB, less than a chunk's 80 KB of K (or V) rows: the
+// K bases move up by 5 sub-blocks at the start of step XKSW and the V bases at step XVSW (and
+// back after the chunk), so that every read of step J, of sub-block SB, is a base register plus
+// the immediate (SB - shift(J)) * 8 KB < 64 KB.
+constexpr int XKSW = 6, XVSW = 8;
+constexpr int XSHIFT = 5 * XSUBB;
+template <int J, int SB> constexpr int k_off() { return (SB - (J >= XKSW ? 5 : 0)) * XSUBB; }
+template <int J, int SB> constexpr int v_off() { return (SB - (J >= XVSW ? 5 : 0)) * XSUBB; }
+template <int V> using I = std::integral_constant<int, V>;
+
+__global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernelArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+
+  // ---- this workgroup's rounds: XCD x (= blockIdx % 8) owns ranks [x G/8, (x+1) G/8)
+  const int G = gridDim.x;
+  const int rank = (G % 8 == 0) ? (int)(blockIdx.x & 7u) * (G / 8) + (int)(blockIdx.x >> 3)
+                                : (int)blockIdx.x;
+  const int nqb = (a.Lq + 31) / 32;       // 32-query blocks per (batch, head)
+  const int rpb = (nqb + XW - 1) / XW;    // rounds per (batch, head)
+  const int64_t R = (int64_t)a.B * a.H * rpb;
+  const int r0 = (int)(R * rank / G), r1 = (int)(R * (rank + 1) / G);
+
+  const SegDesc& sg = a.seg[0];
+  const uint32_t ks = (uint32_t)(sg.ksl * 2), vs = (uint32_t)(sg.vsl * 2);  // row strides, bytes
+  const float c = sreg(a.scale_log2);
+  const float mult_raw = sreg(a.mult_raw);
+  const int64_t lo = a.lo;
+
+  // ---- per-lane LDS addresses
+  const int lds0 = (int)lds_addr(lds);
+  // K fragment s (d = 16s + 8hl .. +7) of sub-block row l32
+  int kb[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) kb[s] = opaque(lds0 + l32 * XROWB + (((2 * s + hl) ^ swz(l32)) << 4));
+  // V transpose reads for d-block db and key half jj (see attn_fwd_bf16.hip)
+  int vb[4][2];
+  {
+    const int s16 = lane & 15, g = (lane >> 4) & 1;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int r = 4 * hl + 8 * jj + (s16 >> 2);
+        const int lc = 4 * db + 2 * g + ((s16 & 3) >> 1);
+        vb[db][jj] = opaque(lds0 + XV0 + r * XROWB + ((lc ^ swz(r)) << 4) + 8 * (s16 & 1));
+      }
+  }
+  // fragment s of K sub-block SB / fragment i of V sub-block SB, as read in step J
+  auto read_k = [&](auto j_c, auto sb_c, int s) -> u32x4 {
+    return lds_read_b128(kb[s] + k_off<decltype(j_c)::value, decltype(sb_c)::value>());
+  };
+  auto read_v = [&](auto j_c, auto sb_c, int i) -> u32x4 {
+    constexpr int OFF = v_off<decltype(j_c)::value, decltype(sb_c)::value>();
+    const int db = i >> 1, m = i & 1;
+    const u32x2 v0 = lds_read_tr16(vb[db][0] + OFF + m * 16 * XROWB);
+    const u32x2 v1 = lds_read_tr16(vb[db][1] + OFF + m * 16 * XROWB);
+    return u32x4{v0[0], v0[1], v1[0], v1[1]};
+  };
+
+  int res_bh = -1, res_ch = -1;  // (batch*head, chunk) resident in LDS
+
+  // Q fragments (B operand of S^T = K Q^T) of round r's item: qf[s] holds d = 16s + 8hl .. +7
+  // of query q0 + l32. The next round's are loaded into qn while this round computes.
+  auto load_q = [&](int r, u32x4 (&dst)[8]) {
+    const int bh = r / rpb, rr = r % rpb;
+    const int b = bh / a.H, h = bh % a.H;
+    const int qb = rr * XW + wave;
+    const int q = qb * 32 + l32;
+    const bool ok = r < r1 && qb < nqb && q < a.Lq;
+    const uint16_t* qp = a.q + a.qsb * b + a.qsl * (int64_t)q + a.qsh * h + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (ok) v = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+      dst[s] = v;
+    }
+  };
+  u32x4 qf[8], qn[8];
+  load_q(r0, qf);
+
+#pragma unroll 1
+  for (int r = r0; r < r1; ++r) {
+    const int bh = r / rpb, rr = r % rpb;
+    const int b = bh / a.H, h = bh % a.H;
+    load_q(r + 1, qn);
+    int64_t hi = a.hi;
+    if (a.k_lens != nullptr) {
+      const int64_t kl = a.k_lens[b];
+      hi = kl < hi ? kl : hi;
+    }
+    const int n_all = hi > lo ? (int)(hi - lo) : 0;  // attended keys (<= 4096, host-checked)
+    const int nch = (n_all + XCH - 1) / XCH;
+    const int qb = rr * XW + wave;
+    const bool active = qb < nqb;
+    const int q0 = qb * 32;
+
+    floatx16 oacc[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) oacc[db][e] = 0.0f;
+    float m_used = M_INIT, lsum = 0.0f;
+
+#pragma unroll 1
+    for (int ch = 0; ch < nch; ++ch) {
+      const int kbase = ch * XCH;                                 // first key of the chunk
+      const int n = n_all - kbase < XCH ? n_all - kbase : XCH;    // keys in the chunk
+      const int nsub = (n + 31) / 32;
+      // dedup: first key of the chunk with the multiplicity bias (1 << 20: none)
+      int mrow = 1 << 20;
+      if (a.mult_key >= 0) {
+        const int64_t mr = a.mult_key - lo - kbase;
+        mrow = mr < 0 ? 0 : (mr > (1 << 20) ? (1 << 20) : (int)mr);
+      }
+
+      if (bh != res_bh || ch != res_ch) {
+        // every wave is past its reads of the old contents
+        barrier_nofence();
+        // rows [kbase, kbase + 32 nsub) of this (b, h) into LDS rows [0, 32 nsub); rows past the
+        // valid keys fetch the last valid key (finite, masked to p = 0 in the softmax)
+        const int64_t row0 = lo + kbase;
+        const unsigned char* kg = reinterpret_cast<const unsigned char*>(sg.k) +
+                                  (sg.ksb * b + sg.ksh * h + sg.ksl * row0) * 2;
+        const unsigned char* vg = reinterpret_cast<const unsigned char*>(sg.v) +
+                                  (sg.vsb * b + sg.vsh * h + sg.vsl * row0) * 2;
+        const int nblk = 8 * nsub;  // 1 KB (4-row) blocks per tensor
+#pragma unroll 1
+        for (int blk = wave; blk < nblk; blk += XW) {
+          const int row = 4 * blk + (lane >> 4);
+          const int src = row < n ? row : n - 1;
+          const uint32_t col = (uint32_t)(((lane & 15) ^ swz(row)) << 4);
+          const uint32_t dst = (uint32_t)lds0 + 1024u * blk;
+          dma16(kg, (uint32_t)src * ks + col, dst);
+          dma16(vg, (uint32_t)src * vs + col, dst + XV0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's rows (and its Q) are in
+        barrier_nofence();
+        res_bh = bh;
+        res_ch = ch;
+      }
+      if (!active || nsub == 0) continue;
+
+      // ---- the pipelined sub-block loop of this chunk
+      floatx16 sA, sB;
+      u32x4 pA[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+      u32x4 pB[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+      bool pend = false;
+      float alpha_p = 1.0f;
+      u32x4 kf[XKR], vf[XVR];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) { sA[e] = 0.0f; sB[e] = 0.0f; }
+      // S_0, and the first K fragments of S_1 and V fragments of PV_0 (read by step 1)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) sA = mfma32x32x16(read_k(I<0>{}, I<0>{}, s), qf[s], sA);
+#pragma unroll
+      for (int i = 0; i < XKA; ++i) kf[i % XKR] = read_k(I<0>{}, I<1>{}, i);
+
+      // One step: softmax of S_J (s_in) into p_out; O += V_{J-1}^T p_in^T (J >= 1); with NEXT,
+      // s_out = S_{J+1} = K_{J+1} Q^T. The first XKA / XVA fragments of a step are read by the
+      // step before it.
+      auto step = [&](auto j_c, auto next_c, floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2],
+                      u32x4 (&p_out)[2]) {
+        constexpr int J = decltype(j_c)::value;
+        constexpr bool NEXT = decltype(next_c)::value;
+        constexpr bool PV = J >= 1;
+        if constexpr (J == XKSW) {
+#pragma unroll
+          for (int s = 0; s < 8; ++s) kb[s] = opaque(kb[s] + XSHIFT);
+        }
+        if constexpr (J == XVSW) {
+#pragma unroll
+          for (int db = 0; db < 4; ++db) {
+            vb[db][0] = opaque(vb[db][0] + XSHIFT);
+            vb[db][1] = opaque(vb[db][1] + XSHIFT);
+          }
+        }
+        if (pend) scale_acc(oacc, alpha_p);
+        if (32 * J + 32 > n || mrow < 32 * J + 32) mask_scores(s_in, J, 0, n, hl, mrow, mult_raw);
+        float ca = -m_used * c;
+        if constexpr (NEXT) {
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s_out[e] = 0.0f;
+        }
+        if constexpr (PV && J == 1) {
+          // PV_0's first fragments (the step before had none to read)
+#pragma unroll
+          for (int i = 0; i < XVA; ++i) vf[i % XVR] = read_v(I<J>{}, I<0>{}, i);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if constexpr (NEXT) {
+            if (i + XKA < 8) kf[(i + XKA) % XKR] = read_k(I<J>{}, I<J + 1>{}, i + XKA);
+            else if (J + 2 < XSB) kf[(i + XKA) % XKR] = read_k(I<J>{}, I<(J + 2 < XSB ? J + 2 : J + 1)>{}, i + XKA - 8);
+          }
+          if constexpr (PV) {
+            if (i + XVA < 8) vf[(i + XVA) % XVR] = read_v(I<J>{}, I<J - 1>{}, i + XVA);
+            else vf[(i + XVA) % XVR] = read_v(I<J>{}, I<J>{}, i + XVA - 8);
+          }
+          if constexpr (NEXT) s_out = mfma32x32x16(kf[i % XKR], qf[i], s_out);
+          if constexpr (PV) oacc[i >> 1] = mfma32x32x16(vf[i % XVR], p_in[i & 1], oacc[i >> 1]);
+        }
+        auto exps = [&]() {
+          float l;
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x0 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e], c, ca));
+              const float x1 = fast_exp2(__builtin_fmaf(s_in[8 * m + 2 * e + 1], c, ca));
+              p_out[m][e] = pack_bf16x2(x0, x1);
+              l = (m == 0 && e == 0) ? x0 + x1 : l + (x0 + x1);
+            }
+          }
+          return l;
+        };
+        float ls = exps();
+        if constexpr (NEXT && PV) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // 2 VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // LDS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          }
+        }
+        asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(ls));
+        // a row sum beyond 2^16 (or not finite) means some p outgrew the reference: move it to
+        // the row max of this sub-block (and the old reference), redo, and rescale O and l
+        bool move = false;
+        float alpha = 1.0f;
+        if (__any(!(ls <= P_LIMIT))) {
+          float mx = s_in[0];
+#pragma unroll
+          for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s_in[e]);
+          mx = wave_max_xor32(mx);
+          const float m_new = fmaxf(mx, m_used);
+          alpha = fast_exp2((m_used - m_new) * c);
+          m_used = m_new;
+          move = true;
+          ca = -m_new * c;
+          ls = exps();
+        }
+        lsum = __builtin_fmaf(lsum, alpha, ls);
+        asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
+        pend = move;
+        alpha_p = alpha;
+      };
+      auto run = [&](auto j_c, floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2],
+                     u32x4 (&p_out)[2]) -> bool {
+        constexpr int J = decltype(j_c)::value;
+        // (every step computes S_{J+1}: a last step without it, as a branch of its own, doubles
+        // the live ranges the register allocator sees and spills; the wasted MFMAs are 8 of the
+        // chunk's 8 + 16 nsub)
+        step(j_c, std::true_type{}, s_in, s_out, p_in, p_out);
+        return J + 1 < nsub;
+      };
+      static_assert(XSB == 10, "the unrolled sub-block sequence below covers 10 sub-blocks");
+      run(I<0>{}, sA, sB, pB, pA) && run(I<1>{}, sB, sA, pA, pB) && run(I<2>{}, sA, sB, pB, pA) &&
+          run(I<3>{}, sB, sA, pA, pB) && run(I<4>{}, sA, sB, pB, pA) &&
+          run(I<5>{}, sB, sA, pA, pB) && run(I<6>{}, sA, sB, pB, pA) &&
+          run(I<7>{}, sB, sA, pA, pB) && run(I<8>{}, sA, sB, pB, pA) && run(I<9>{}, sB, sA, pA, pB);
+      // drain: O += V_J^T P_J^T of the chunk's last sub-block J = nsub - 1 (P_J is in pA for
+      // even J, pB for odd), with the V bases as step J left them
+      {
+        if (pend) scale_acc(oacc, alpha_p);
+        pend = false;
+        const int jl = nsub - 1;
+        const int voff = (jl - (jl >= XVSW ? 5 : 0)) * XSUBB;
+        u32x4 pl[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pl[m][e] = (jl & 1) ? pB[m][e] : pA[m][e];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int db = i >> 1, m = i & 1;
+          const u32x2 v0 = lds_read_tr16(vb[db][0] + voff + m * 16 * XROWB);
+          const u32x2 v1 = lds_read_tr16(vb[db][1] + voff + m * 16 * XROWB);
+          oacc[db] = mfma32x32x16(u32x4{v0[0], v0[1], v1[0], v1[1]}, pl[m], oacc[db]);
+        }
+      }
+      // the bases back where the next chunk's step 0 expects them
+      if (nsub > XKSW) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kb[s] = opaque(kb[s] - XSHIFT);
+      }
+      if (nsub > XVSW) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          vb[db][0] = opaque(vb[db][0] - XSHIFT);
+          vb[db][1] = opaque(vb[db][1] - XSHIFT);
+        }
+      }
+    }
+    if (!active) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) qf[s] = qn[s];
+      continue;
+    }
+
+    // ---- epilogue: O / l, straight from registers. Lane (l32, hl) holds d = 32 db + 8 g + 4 hl
+    // .. +3 of query q0 + l32; one exchange with lane ^ 32 gives each lane 8 consecutive d
+    // (16 bytes) for the bf16 store.
+    const float l_tot = wave_sum_xor32(lsum);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const int q = q0 + l32;
+    if (a.o32) {
+      float* op = reinterpret_cast<float*>(a.out) + a.osb * b + a.osl * (int64_t)q + a.osh * h;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          floatx4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = oacc[db][4 * g + e] * inv;
+          if (q < a.Lq) *reinterpret_cast<floatx4*>(op + 32 * db + 8 * g + 4 * hl) = w;
+        }
+    } else {
+      uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)q + a.osh * h;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int gx = 2 * k, gy = 2 * k + 1;
+          const uint32_t x0 = pack_bf16x2(oacc[db][4 * gx] * inv, oacc[db][4 * gx + 1] * inv);
+          const uint32_t x1 = pack_bf16x2(oacc[db][4 * gx + 2] * inv, oacc[db][4 * gx + 3] * inv);
+          const uint32_t y0 = pack_bf16x2(oacc[db][4 * gy] * inv, oacc[db][4 * gy + 1] * inv);
+          const uint32_t y1 = pack_bf16x2(oacc[db][4 * gy + 2] * inv, oacc[db][4 * gy + 3] * inv);
+          const uint32_t r0v = (uint32_t)__shfl_xor((int)(hl ? x0 : y0), 32);
+          const uint32_t r1v = (uint32_t)__shfl_xor((int)(hl ? x1 : y1), 32);
+          const u32x4 w = hl ? u32x4{r0v, r1v, y0, y1} : u32x4{x0, x1, r0v, r1v};
+          if (q < a.Lq) {
+            uint16_t* p = op + 32 * db + 16 * k + 8 * hl;
+            if (a.o16) {
+              *reinterpret_cast<u32x4*>(p) = w;
+            } else {
+              *reinterpret_cast<u32x2*>(p) = u32x2{w[0], w[1]};
+              *reinterpret_cast<u32x2*>(p + 4) = u32x2{w[2], w[3]};
+            }
+          }
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = qn[s];
+  }
+}
+
+}  // namespace
+
+int cross_attn_max_keys_resident() { return XCH; }
+
+hipError_t launch_cross_attn(const AttnKernelArgs& a, int num_cus, hipStream_t stream) {
+  static hipError_t attr = hipFuncSetAttribute((const void*)cross_attn_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, XLDS);
+  if (attr != hipSuccess) return attr;
+  const int nqb = (a.Lq + 31) / 32;
+  const int64_t rounds = (int64_t)a.B * a.H * ((nqb + XW - 1) / XW);
+  int64_t g = rounds < num_cus ? rounds : num_cus;
+  if (g >= 8) g -= g % 8;  // a multiple of 8: each XCD gets an equal share of the ranks
+  if (g < 1) g = 1;
+  hipLaunchKernelGGL(cross_attn_kernel, dim3((uint32_t)g), dim3(XW * 64), XLDS, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace lbw

@@ -1,0 +1,129 @@
+"""GPU parity of the cross-attention kernel (cross_attn.hip, lbw_cross_attention_fwd and the
+dedup entry point) against the fp32 oracle.
+
+The kernel keeps a (batch, head)'s K/V rows resident in LDS when at most 320 keys are attended
+and otherwise walks them in 320-key chunks, with persistent workgroups that run consecutive
+256-query rounds. The cases cover both paths and their edges: key counts around the 32-key
+sub-block and the 320-key chunk, per-batch valid lengths (k_lens) that put one batch on each
+path, windows, query counts that leave partial 32-query blocks and rounds, head counts whose
+rounds straddle workgroups, strided views, the bf16 bar and, on the fp32 output, the bound the
+kernel's arithmetic fixes (P enters the PV product as bf16: |o - o_exact| <= 2^-8 max|V|)."""
+import math
+
+import pytest
+import torch
+
+import oracle as O
+from parity import assert_parity
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _kernel_bound(v):
+    return float(v.float().abs().max()) * 2.0 ** -8 * 1.01 + 1e-5
+
+
+def _qkv(B, Lq, H, L, seed, qgain=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, Lq, H, 128, generator=g) * qgain).to(torch.bfloat16)
+    k = torch.randn(B, L, H, 128, generator=g).to(torch.bfloat16)
+    v = (0.5 * torch.randn(B, L, H, 128, generator=g)).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,Lq,H,L,lens", [
+    (1, 1, 1, 1, None),
+    (1, 33, 2, 31, None),
+    (1, 64, 1, 32, None),
+    (1, 100, 3, 33, None),
+    (1, 257, 2, 300, None),
+    (1, 300, 2, 319, None),
+    (1, 513, 2, 320, None),
+    (1, 96, 2, 321, None),           # chunked: 320 + 1
+    (1, 200, 3, 640, None),          # two full chunks
+    (2, 130, 2, 700, [0, 700]),      # one batch with no keys (output 0), one chunked
+    (2, 333, 4, 512, [300, 512]),    # resident and chunked batches in one call
+    (3, 77, 5, 4096, [1, 4096, 333]),
+])
+def test_cross_matches_oracle(lib, B, Lq, H, L, lens):
+    from lbw_amd import cross_attention
+    q, k, v = _qkv(B, Lq, H, L, seed=Lq + L + H)
+    kl = None if lens is None else torch.tensor(lens, dtype=torch.int32)
+    print(f"case B={B} Lq={Lq} H={H} L={L} k_lens={lens}", flush=True)
+    out = cross_attention(q.to(DEV), k.to(DEV), v.to(DEV),
+                          k_lens=None if kl is None else kl.to(DEV))
+    ref = O.attention_ref(q, k, v, k_lens=kl)
+    assert_parity(out, ref, "cross")
+
+
+@pytest.mark.parametrize("H,Lq", [(40, 4680), (7, 1000)])
+def test_cross_rounds_across_workgroups_fp32(lib, H, Lq):
+    """Many heads (rounds of one head spread over several workgroups, workgroups spanning two
+    heads, the K/V reload at each switch) on the fp32 output, against the arithmetic bound;
+    peaked queries (gain 4) so that the exponent reference moves. Sampled rows of every 5th
+    head, including the partial last 32-query block."""
+    from lbw_amd import attention_segments
+    q, k, v = _qkv(1, Lq, H, 512, seed=H, qgain=4.0)
+    kl = torch.tensor([300], dtype=torch.int32)
+    out = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV))], k_lens=kl.to(DEV), cross=True,
+                             out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    tail = torch.arange((Lq // 32) * 32, Lq)
+    sel = torch.cat([torch.randperm(Lq, generator=torch.Generator().manual_seed(H))[:200], tail])
+    sel = sel.unique().sort().values
+    oc = out[:, sel].cpu()
+    for h in range(0, H, 5):
+        ref = O.attention_ref(q[:, sel][:, :, h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1], k_lens=kl)
+        err = float((oc[:, :, h:h + 1] - ref).abs().max())
+        bound = _kernel_bound(v[:, :300, h])
+        assert err <= bound, (h, err, bound)
+
+
+def test_cross_window_and_strided_views(lib):
+    """A key window [lo, hi) on a context held as column views of a fused [L, 2, H, D] buffer,
+    q and out as strided views; bf16 output."""
+    from lbw_amd import attention_segments
+    g = torch.Generator().manual_seed(17)
+    B, Lq, H, L = 2, 150, 3, 600
+    kv = torch.randn(B, L, 2, H, 128, generator=g).to(torch.bfloat16)
+    qx = torch.randn(B, Lq, 2, H, 128, generator=g).to(torch.bfloat16)
+    q, k, v = qx[:, :, 0], kv[:, :, 0], kv[:, :, 1]
+    d_kv, d_qx = kv.to(DEV), qx.to(DEV)
+    for lo, hi in [(100, 400), (10, 600), (333, 334)]:
+        out = attention_segments(d_qx[:, :, 0], [(d_kv[:, :, 0], d_kv[:, :, 1])], kv_lo=lo,
+                                 kv_hi=hi, cross=True)
+        assert_parity(out, O.attention_ref(q, k, v, kv_lo=lo, kv_hi=hi), f"window {lo}-{hi}")
+
+
+def test_cross_full_size_wan14b_480p(lib):
+    """The 14B 480p cross-attention at full size: 4680 queries x 40 heads over a 512-row context
+    with rows 300.. identical (the projected zero padding); masked to 300 rows, unmasked, and
+    the exact dedup, on sampled rows of 4 heads (bf16 bar), plus the dedup result against the
+    unmasked one."""
+    from lbw_amd import cross_attention, padding_start
+    g = torch.Generator(device=DEV).manual_seed(23)
+    H, Lq, L, nv = 40, 4680, 512, 300
+    q = torch.randn(1, Lq, H, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(1, L, H, 128, generator=g, device=DEV)
+    v = 0.5 * torch.randn(1, L, H, 128, generator=g, device=DEV)
+    k[:, nv:] = k[:, L - 1:]
+    v[:, nv:] = v[:, L - 1:]
+    k, v = k.to(torch.bfloat16), v.to(torch.bfloat16)
+    kl = torch.tensor([nv], dtype=torch.int32, device=DEV)
+    nd = padding_start(k, v)
+    assert nd == nv
+    outs = {"masked": cross_attention(q, k, v, k_lens=kl),
+            "unmasked": cross_attention(q, k, v),
+            "dedup": cross_attention(q, k, v, n_distinct=nd)}
+    torch.cuda.synchronize()
+    sel = torch.cat([torch.randperm(Lq, generator=torch.Generator().manual_seed(5))[:256],
+                     torch.arange(4672, Lq)]).unique().sort().values
+    qc, kc, vc = q[:, sel].cpu(), k.cpu(), v.cpu()
+    for h in (0, 13, 26, 39):
+        for name, out in outs.items():
+            ref = O.attention_ref(qc[:, :, h:h + 1], kc[:, :, h:h + 1], vc[:, :, h:h + 1],
+                                  k_lens=torch.tensor([nv]) if name == "masked" else None)
+            m = assert_parity(out[:, sel][:, :, h:h + 1], ref, f"{name} head {h}")
+            print(f"  {name} head {h}: {m}", flush=True)
+    assert float((outs["dedup"].float() - outs["unmasked"].float()).abs().max()) <= 1e-2

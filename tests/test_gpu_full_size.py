@@ -11,8 +11,8 @@ heads spread over the head range, to the bf16 bar of every parity test here.
 
 The same call with fp32 output (the normalised O / l before its bf16 rounding, same kernels and
 plan) is held to the bound that the kernel's own arithmetic fixes: P enters the PV product as
-bf16 (relative rounding <= 2^-9) while the row sum adds the fp32 p, so |o - o_exact| <=
-2^-9 max|V| per head; everything else is fp32. This isolates the kernel from the output
+bf16 (relative rounding <= 2^-8) while the row sum adds the fp32 p, so |o - o_exact| <=
+2^-8 max|V| per head; everything else is fp32. This isolates the kernel from the output
 rounding, and holds for peaked heads too (RMSNorm gains up to 16 on q, where the reference
 moves inside rows), whose |o| near 2-4 no bf16 output can meet 1e-2 for."""
 import math
@@ -43,8 +43,8 @@ def _splits_of(q4, segs):
 
 
 def _kernel_bound(v_head):
-    """2^-9 max|V| (one bf16 rounding of P), plus fp32 accumulation slack."""
-    return float(v_head.float().abs().max()) * 2.0 ** -9 * 1.01 + 1e-5
+    """2^-8 max|V| (one bf16 rounding of P), plus fp32 accumulation slack."""
+    return float(v_head.float().abs().max()) * 2.0 ** -8 * 1.01 + 1e-5
 
 
 def _pipeline(H, grid, start_frame, cached, heads, rows, seed, two_segments,
