@@ -354,6 +354,32 @@ def counter_workload():
     print("counter workload done", flush=True)
 
 
+def cross_workload():
+    """The program the cross-attention profiles run: 5 calls each of the 14B 480p
+    cross-attention (4680 q x 40 heads over a 512-row context, rows 300.. identical) masked to
+    300 rows, unmasked (512 keys) and the exact dedup, on seeded inputs."""
+    import torch
+    from lbw_amd import cross_attention, padding_start
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(1, 4680, 40, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(1, 512, 40, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(1, 512, 40, D, generator=g, device=dev).to(torch.bfloat16)
+    k[:, 300:] = k[:, 511:]
+    v[:, 300:] = v[:, 511:]
+    kl = torch.tensor([300], dtype=torch.int32, device=dev)
+    nd = padding_start(k, v)
+    for _ in range(5):
+        cross_attention(q, k, v, k_lens=kl)
+    for _ in range(5):
+        cross_attention(q, k, v)
+    for _ in range(5):
+        cross_attention(q, k, v, n_distinct=nd)
+    torch.cuda.synchronize()
+    print("cross workload done", flush=True)
+
+
 def _pmc_rows(d, counter):
     """Per-dispatch values of `counter` from a rocprofv3 --pmc csv output directory."""
     files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
@@ -434,6 +460,8 @@ def main():
                     help="skip the timings of the other workload shapes")
     ap.add_argument("--counter-workload", action="store_true",
                     help="5 pre-scaled chunk attention calls (the program of the SQ counter passes)")
+    ap.add_argument("--cross-workload", action="store_true",
+                    help="5 calls each of the 14B 480p cross-attention, masked / unmasked / dedup")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the program profiled by the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -454,6 +482,9 @@ def main():
         return
     if args.pmc_workload:
         pmc_workload()
+        return
+    if args.cross_workload:
+        cross_workload()
         return
 
     import torch

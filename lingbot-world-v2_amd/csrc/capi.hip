@@ -255,6 +255,10 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
     if (s0.k_stride_l * 2 * cross_attn_max_keys_resident() >= (int64_t(1) << 32) ||
         s0.v_stride_l * 2 * cross_attn_max_keys_resident() >= (int64_t(1) << 32))
       return fail(LBW_ERR_UNSUPPORTED, "cross-attention: K/V row stride too large");
+    // Q and O rows of one (batch, head) are addressed with 31-bit byte offsets (buffer ranges)
+    const int64_t rows = (int64_t)p->lq + 512;
+    if (rows * p->q_stride_l * 2 >= (int64_t(1) << 31) || rows * p->o_stride_l * 4 >= (int64_t(1) << 31))
+      return fail(LBW_ERR_UNSUPPORTED, "cross-attention: q/out rows span more than 2 GiB");
     hipError_t e = launch_cross_attn(a, num_cus(), st);
     if (e != hipSuccess) return hip_fail(e, "cross-attention kernel launch");
     return LBW_OK;

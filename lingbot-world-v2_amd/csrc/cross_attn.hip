@@ -50,6 +50,20 @@ template <int J, int SB> constexpr int k_off() { return (SB - (J >= XKSW ? 5 : 0
 template <int J, int SB> constexpr int v_off() { return (SB - (J >= XVSW ? 5 : 0)) * XSUBB; }
 template <int V> using I = std::integral_constant<int, V>;
 
+// A wave-uniform int32 read through the scalar cache. As a vector load, the compiler waits for
+// it with vmcnt(0), which would also wait for the Q prefetch and the output stores in flight.
+__device__ __forceinline__ int load_scalar_i32(const int32_t* p) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+
+// OUT: the output form, a template parameter so that the epilogue has one store sequence and
+// the compiler counts its stores exactly. 0: bf16 with 16-byte stores (aligned out, strides
+// multiples of 8); 1: bf16 with 8-byte stores; 2: fp32.
+enum { kOutBf16x16 = 0, kOutBf16x8 = 1, kOutF32 = 2 };
+
+template <int OUT>
 __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernelArgs a) {
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
@@ -106,20 +120,22 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
   int res_bh = -1, res_ch = -1;  // (batch*head, chunk) resident in LDS
 
   // Q fragments (B operand of S^T = K Q^T) of round r's item: qf[s] holds d = 16s + 8hl .. +7
-  // of query q0 + l32. The next round's are loaded into qn while this round computes.
+  // of query q0 + l32. The next round's are loaded into qn while this round computes. Q and O
+  // go through buffer loads and stores whose range check covers the (b, h) rows [0, Lq): rows
+  // past Lq (a partial last block, waves with no item) load 0 and store nothing with no branch,
+  // so the compiler counts the loads and stores in flight exactly and waits for the prefetch
+  // only, not for every store before it.
   auto load_q = [&](int r, u32x4 (&dst)[8]) {
-    const int bh = r / rpb, rr = r % rpb;
+    const int bh = r < r1 ? r / rpb : 0, rr = r % rpb;
     const int b = bh / a.H, h = bh % a.H;
-    const int qb = rr * XW + wave;
-    const int q = qb * 32 + l32;
-    const bool ok = r < r1 && qb < nqb && q < a.Lq;
-    const uint16_t* qp = a.q + a.qsb * b + a.qsl * (int64_t)q + a.qsh * h + 8 * hl;
+    const int q = (rr * XW + wave) * 32 + l32;
+    const uint32_t bytes = r < r1 ? (uint32_t)a.Lq * (uint32_t)(a.qsl * 2) : 0u;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.q + a.qsb * b + a.qsh * h), (short)0, (int)bytes, 0x00020000);
+    const uint32_t off = (uint32_t)(q * a.qsl + 8 * hl) * 2u;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (ok) v = *reinterpret_cast<const u32x4*>(qp + 16 * s);
-      dst[s] = v;
-    }
+    for (int s = 0; s < 8; ++s)
+      dst[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 32 * s, 0, 0));
   };
   u32x4 qf[8], qn[8];
   load_q(r0, qf);
@@ -131,7 +147,7 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
     load_q(r + 1, qn);
     int64_t hi = a.hi;
     if (a.k_lens != nullptr) {
-      const int64_t kl = a.k_lens[b];
+      const int64_t kl = load_scalar_i32(a.k_lens + b);
       hi = kl < hi ? kl : hi;
     }
     const int n_all = hi > lo ? (int)(hi - lo) : 0;  // attended keys (<= 4096, host-checked)
@@ -339,20 +355,19 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
         }
       }
     }
-    if (!active) {
-#pragma unroll
-      for (int s = 0; s < 8; ++s) qf[s] = qn[s];
-      continue;
-    }
-
     // ---- epilogue: O / l, straight from registers. Lane (l32, hl) holds d = 32 db + 8 g + 4 hl
     // .. +3 of query q0 + l32; one exchange with lane ^ 32 gives each lane 8 consecutive d
-    // (16 bytes) for the bf16 store.
+    // (16 bytes) for the bf16 store. Rows past Lq (and waves with no item) store nothing: the
+    // buffer range check drops them.
     const float l_tot = wave_sum_xor32(lsum);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     const int q = q0 + l32;
-    if (a.o32) {
-      float* op = reinterpret_cast<float*>(a.out) + a.osb * b + a.osl * (int64_t)q + a.osh * h;
+    constexpr int esz = OUT == kOutF32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<unsigned char*>(a.out) + (a.osb * b + a.osh * h) * esz), (short)0,
+        (int)((uint32_t)a.Lq * (uint32_t)(a.osl * esz)), 0x00020000);
+    const uint32_t orow = (uint32_t)(q * a.osl) * (uint32_t)esz;
+    if constexpr (OUT == kOutF32) {
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -360,10 +375,10 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
           floatx4 w;
 #pragma unroll
           for (int e = 0; e < 4; ++e) w[e] = oacc[db][4 * g + e] * inv;
-          if (q < a.Lq) *reinterpret_cast<floatx4*>(op + 32 * db + 8 * g + 4 * hl) = w;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, w), ro,
+                                                 orow + 4 * (32 * db + 8 * g + 4 * hl), 0, 0);
         }
     } else {
-      uint16_t* op = a.out + a.osb * b + a.osl * (int64_t)q + a.osh * h;
 #pragma unroll
       for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -376,14 +391,12 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
           const uint32_t r0v = (uint32_t)__shfl_xor((int)(hl ? x0 : y0), 32);
           const uint32_t r1v = (uint32_t)__shfl_xor((int)(hl ? x1 : y1), 32);
           const u32x4 w = hl ? u32x4{r0v, r1v, y0, y1} : u32x4{x0, x1, r0v, r1v};
-          if (q < a.Lq) {
-            uint16_t* p = op + 32 * db + 16 * k + 8 * hl;
-            if (a.o16) {
-              *reinterpret_cast<u32x4*>(p) = w;
-            } else {
-              *reinterpret_cast<u32x2*>(p) = u32x2{w[0], w[1]};
-              *reinterpret_cast<u32x2*>(p + 4) = u32x2{w[2], w[3]};
-            }
+          const uint32_t off = orow + 2 * (32 * db + 16 * k + 8 * hl);
+          if constexpr (OUT == kOutBf16x16) {
+            __builtin_amdgcn_raw_buffer_store_b128(w, ro, off, 0, 0);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{w[0], w[1]}, ro, off, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{w[2], w[3]}, ro, off + 8, 0, 0);
           }
         }
     }
@@ -396,16 +409,27 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
 
 int cross_attn_max_keys_resident() { return XCH; }
 
-hipError_t launch_cross_attn(const AttnKernelArgs& a, int num_cus, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)cross_attn_kernel,
+template <int OUT>
+static hipError_t set_lds_attr() {
+  static hipError_t attr = hipFuncSetAttribute((const void*)cross_attn_kernel<OUT>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, XLDS);
+  return attr;
+}
+
+hipError_t launch_cross_attn(const AttnKernelArgs& a, int num_cus, hipStream_t stream) {
+  const int out = a.o32 ? kOutF32 : (a.o16 ? kOutBf16x16 : kOutBf16x8);
+  hipError_t attr = out == kOutF32 ? set_lds_attr<kOutF32>()
+                    : out == kOutBf16x16 ? set_lds_attr<kOutBf16x16>() : set_lds_attr<kOutBf16x8>();
   if (attr != hipSuccess) return attr;
   const int nqb = (a.Lq + 31) / 32;
   const int64_t rounds = (int64_t)a.B * a.H * ((nqb + XW - 1) / XW);
   int64_t g = rounds < num_cus ? rounds : num_cus;
   if (g >= 8) g -= g % 8;  // a multiple of 8: each XCD gets an equal share of the ranks
   if (g < 1) g = 1;
-  hipLaunchKernelGGL(cross_attn_kernel, dim3((uint32_t)g), dim3(XW * 64), XLDS, stream, a);
+  const dim3 grid((uint32_t)g), block(XW * 64);
+  if (out == kOutF32) hipLaunchKernelGGL(cross_attn_kernel<kOutF32>, grid, block, XLDS, stream, a);
+  else if (out == kOutBf16x16) hipLaunchKernelGGL(cross_attn_kernel<kOutBf16x16>, grid, block, XLDS, stream, a);
+  else hipLaunchKernelGGL(cross_attn_kernel<kOutBf16x8>, grid, block, XLDS, stream, a);
   return hipGetLastError();
 }
 
