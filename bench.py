@@ -380,6 +380,27 @@ def cross_workload():
     print("cross workload done", flush=True)
 
 
+def fp8_workload():
+    """The program the fp8-cache profiles run: 5 calls of the 14B 720p long-horizon chunk
+    (3600 q x 40 heads over 90000 keys) on an fp8-e4m3 cache, then 5 on the same keys as a bf16
+    cache, on seeded inputs."""
+    import torch
+    from lbw_amd import attention_fp8kv, attention_segments, quantize_kv_fp8
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(1, 3600, 40, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(1, 90000, 40, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(1, 90000, 40, D, generator=g, device=dev).to(torch.bfloat16)
+    k8, v8 = quantize_kv_fp8(k), quantize_kv_fp8(v)
+    for _ in range(5):
+        attention_fp8kv(q, [(k8, v8)])
+    for _ in range(5):
+        attention_segments(q, [(k, v)])
+    torch.cuda.synchronize()
+    print("fp8 workload done", flush=True)
+
+
 def _pmc_rows(d, counter):
     """Per-dispatch values of `counter` from a rocprofv3 --pmc csv output directory."""
     files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
@@ -462,6 +483,8 @@ def main():
                     help="5 pre-scaled chunk attention calls (the program of the SQ counter passes)")
     ap.add_argument("--cross-workload", action="store_true",
                     help="5 calls each of the 14B 480p cross-attention, masked / unmasked / dedup")
+    ap.add_argument("--fp8-workload", action="store_true",
+                    help="5 calls of the 14B 720p long-horizon chunk on an fp8 cache, 5 on bf16")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="run the program profiled by the FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -485,6 +508,9 @@ def main():
         return
     if args.cross_workload:
         cross_workload()
+        return
+    if args.fp8_workload:
+        fp8_workload()
         return
 
     import torch

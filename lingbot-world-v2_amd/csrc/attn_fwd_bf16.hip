@@ -56,6 +56,78 @@ constexpr int NDMA = TILE_B / (NWAVE * 64 * 16);  // 16-byte DMA blocks per lane
 constexpr int K_AHEAD = 2, V_AHEAD = 2;
 static_assert(NSTAGE * TILE_B <= V_BASE, "K tiles must fit below the V tiles");
 
+// fp8 cache: K tiles of e4m3 codes (128-byte rows, 8 KB), then two staging slots per wave for
+// the V codes (1 KB) and the tile's two block scales (256 B); the V tiles are bf16 as above.
+constexpr int ROWB8 = D;                              // bytes per fp8 K row in LDS
+constexpr int TILE8_B = BN * ROWB8;                   // 8 KB
+constexpr int HALF8_B = TILE8_B / 2;
+constexpr int RAW_BASE = NSTAGE * TILE8_B;            // + slot * TILE8_B + 1 KB * wave
+constexpr int SC_BASE = RAW_BASE + 2 * TILE8_B;       // + slot * SC_SLOT_B + 256 B * wave
+constexpr int SC_SLOT_B = NWAVE * 256;
+static_assert(SC_BASE + 2 * SC_SLOT_B <= V_BASE, "fp8 staging must fit below the V tiles");
+static_assert(TILE8_B == NWAVE * 64 * 16, "one 16-byte copy per lane per fp8 tile");
+
+// LDS swizzle of the 128-byte fp8 K rows: 16-byte chunk c of row r at chunk c ^ swz8(r). The
+// QK operand reads (lane (l32, h): row l32, chunk 4m + 2i + h) are then conflict-free: of any
+// 16 consecutive lanes, the rows of one parity land on 8 distinct chunks.
+__device__ __forceinline__ int swz8(int r) { return (r >> 1) & 7; }
+
+// Waits until at most n of this wave's copies are in flight (n in 0..2).
+__device__ __forceinline__ void wait_vm(int n) {
+  if (n <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  else if (n == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+}
+
+// S^T += K Q^T on the fp8 matrix cores: v_mfma_scale_f32_32x32x64_f8f6f4 with both operands
+// e4m3 (format 0). Operand byte j of lane (l32, h) is d = 64m + 16h + j (j < 16) or
+// 64m + 32 + 16h + (j - 16) (j >= 16) of d-half m, for the K row and the query column alike;
+// the query's operand carries the e8m0 scale `qscale` (2^(qscale - 127)), K's is 1 (127).
+__device__ __forceinline__ floatx16 mfma_qk8(const i32x8& k, const i32x8& q, const floatx16& c,
+                                             int qscale) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(k, q, c, 0, 0, 0, 127, 0, qscale);
+}
+
+// The query operand of the fp8 QK product: the lane's 64 bf16 values of its query (qf[4m + 2r +
+// half] holds d = 64m + 32r + 16h + 8 half .. +7) as q = (hi + lo / 16) 2^e per query, hi and lo
+// e4m3, e = floor(log2 max|q|) - 7 (so |q| 2^-e < 256 and |lo| <= 128, both inside e4m3's
+// range). hi carries q's leading 4 significant bits and lo the next 4, so the pair holds a bf16
+// value exactly unless it is below 2^-13 of the row's max (then the error is below 2^-21 of it).
+// Returns 127 + e, the e8m0 scale of hi (lo's is 4 less).
+__device__ __forceinline__ int q8_split(const u32x4 (&qf)[8], i32x8 (&qh)[2], i32x8 (&ql)[2]) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      amax = fmaxf(amax, fmaxf(fabsf(bf16_lo(qf[s][w])), fabsf(bf16_hi(qf[s][w]))));
+  amax = wave_max_xor32(amax);  // lanes l and l^32 hold the two halves of one query
+  int e = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127 - 7;
+  e = e < -120 ? -120 : (e > 120 ? 120 : e);
+  const float sc = __uint_as_float((uint32_t)(127 - e) << 23);  // 2^-e, exact
+#pragma unroll
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      // operand word w = bytes 4w .. 4w+3: run w / 4, elements 4 (w % 4) .. +3 of the run
+      const int e0 = 4 * (w & 3);
+      const u32x4& src = qf[4 * m + 2 * (w >> 2) + (e0 >> 3)];
+      const uint32_t w0 = src[(e0 & 7) >> 1], w1 = src[((e0 & 7) >> 1) + 1];
+      const float x0 = bf16_lo(w0) * sc, x1 = bf16_hi(w0) * sc;
+      const float x2 = bf16_lo(w1) * sc, x3 = bf16_hi(w1) * sc;
+      int hw = __builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false);
+      hw = __builtin_amdgcn_cvt_pk_fp8_f32(x2, x3, hw, true);
+      // the residuals x - hi are exact in fp32 (x has 8 significant bits)
+      const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hw, false);
+      const auto h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hw, true);
+      int lw = __builtin_amdgcn_cvt_pk_fp8_f32((x0 - h01[0]) * 16.0f, (x1 - h01[1]) * 16.0f, 0, false);
+      lw = __builtin_amdgcn_cvt_pk_fp8_f32((x2 - h23[0]) * 16.0f, (x3 - h23[1]) * 16.0f, lw, true);
+      qh[m][w] = hw;
+      ql[m][w] = lw;
+    }
+  return 127 + e;
+}
+
 // Waits until at most `n` tiles' DMA groups (2*NDMA loads each) of this wave are in flight.
 __device__ __forceinline__ void wait_tiles_outstanding(int n) {
   static_assert(2 * NDMA == 4, "vmcnt immediates below assume 4 loads per tile");
@@ -97,10 +169,14 @@ __global__ void __launch_bounds__(64) attn_queue_reset_kernel(uint32_t* q) {
 }
 
 // FP8 = false: bf16 K/V, DMA'd straight into LDS. FP8 = true: e4m3 K/V codes with fp32 scales
-// per (batch, head, 64-token block): each tile is loaded into registers one tile ahead,
-// converted exactly to bf16 (every e4m3 value is a bf16 value) and written into the same LDS
-// layout; the block scales fold into the softmax (K's into the exponent's multiplier, V's into
-// its addend as log2, and out of the row sum), so the MFMA loop is the bf16 one.
+// per (batch, head, 64-token block). The K codes are copied into LDS as they are and S^T = K Q^T
+// runs on the fp8 matrix cores, against Q split into two e4m3 operands (q8_split): four x64
+// MFMAs per 32-key sub-block instead of eight bf16 ones, half the K bytes in LDS and no K
+// conversion. The V codes and the tile's two scales go through a per-wave LDS staging slot
+// (copied two steps ahead); the wave that copied them converts its rows exactly to bf16 (every
+// e4m3 value is a bf16 value) into the bf16 V tile, so P stays bf16 in the PV product. The block
+// scales fold into the softmax (K's into the exponent's multiplier, V's into its addend as log2,
+// and out of the row sum).
 // FOLD: scale * log2(e) == 1, i.e. q already carries log2(e)/sqrt(d) (a pre-scaled q, as the
 // fused q/k kernel writes it): the QK chain starts from -m instead of 0, so the MFMA result is
 // already the exponent of p and the softmax needs no per-score FMA (see the step).
@@ -144,15 +220,17 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   const int q0 = qt * BM + wave * 32;  // first query of this wave (wave-uniform)
   const bool wave_active = q0 < a.Lq;
 
-  // ---- Q fragments (B operand of S^T = K Q^T): qf[s] holds d = 16s + 8hl .. +7
+  // ---- Q fragments (B operand of S^T = K Q^T): qf[s] holds d = 16s + 8hl .. +7; for the fp8
+  // operands (q8_split) d = 32 (s / 2) + 16hl + 8 (s % 2) .. +7
   u32x4 qf[8];
   {
     const int q = q0 + l32;
-    const uint16_t* qp = a.q + a.qsb * b + a.qsl * (int64_t)q + a.qsh * h + 8 * hl;
+    const uint16_t* qp = a.q + a.qsb * b + a.qsl * (int64_t)q + a.qsh * h;
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
+      const int d0 = FP8 ? 32 * (s >> 1) + 16 * hl + 8 * (s & 1) : 16 * s + 8 * hl;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (q < a.Lq) v = *reinterpret_cast<const u32x4*>(qp + 16 * s);
+      if (q < a.Lq) v = *reinterpret_cast<const u32x4*>(qp + d0);
       qf[s] = v;
     }
     // (waited for below, together with the first K/V tiles: one round trip, not two)
@@ -179,11 +257,18 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     dma_col[i] = ((lane & 15) ^ swz(dma_row[i])) * 16;  // byte offset of the logical chunk
   }
   // LDS byte addresses of this lane's fragments in stage 0.
-  // K fragment (sub-block rows 0..31) for d-slice s: row l32, logical chunk 2s + hl.
+  // K fragment (sub-block rows 0..31) for d-slice s: row l32, logical chunk 2s + hl. fp8: the
+  // x64 operand of d-half m is the two 16-byte reads koff[2m] (bytes 0-15, chunk 4m + hl) and
+  // koff[2m + 1] (bytes 16-31, chunk 4m + 2 + hl), the same formula over 128-byte rows.
   const int lds0 = (int)lds_addr(lds);
   int koff[8];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) koff[s] = opaque(lds0 + l32 * ROWB + (((2 * s + hl) ^ swz(l32)) << 4));
+  for (int s = 0; s < 8; ++s) {
+    if constexpr (FP8)
+      koff[s] = s < 4 ? opaque(lds0 + l32 * ROWB8 + (((2 * s + hl) ^ swz8(l32)) << 4)) : 0;
+    else
+      koff[s] = opaque(lds0 + l32 * ROWB + (((2 * s + hl) ^ swz(l32)) << 4));
+  }
   // V transpose reads (sub-block rows 0..31, k-step m = 0) for d-block db and key
   // half j: source row 4hl + 8j + s/4, columns 32db + 16g + 4(s%4) .. +3 (s = lane % 16,
   // g = (lane / 16) % 2).
@@ -255,39 +340,60 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     return rows;
   };
 
-  // fp8: thread t stages row t/8, 16-byte code chunk t%8 (bf16 logical chunks 2(t%8), +1) of
-  // the K and V tiles; loads go to registers (k8, v8) and scales to sk_n / sv_n.
+  // fp8: thread t (= 64 wave + lane) copies row t / 8, 16-byte code chunk t % 8 of each tile:
+  // K codes into the K tile (at physical chunk t % 8, so the logical chunk is (t % 8) ^ swz8),
+  // V codes into its wave's staging slot (at 16 lane), and lanes 0 / 1 copy the K / V block
+  // scale (dwords 0 and 1 of the wave's scale slot). Rows outside a partial tile's valid range
+  // fetch a valid row instead, as above. The copying wave converts its own staged V rows.
   const int row8 = threadIdx.x >> 3, j8 = threadIdx.x & 7;
-  u32x4 k8 = {0u, 0u, 0u, 0u}, v8 = {0u, 0u, 0u, 0u};
-  float sk_n = 1.0f, sv_n = 1.0f;
-  auto issue8 = [&]() -> int {
+  const int kcol8 = (j8 ^ swz8(row8)) << 4;
+  const uint32_t raw_wave = lds_addr(lds) + RAW_BASE + 1024 * wave;  // + slot * TILE8_B
+  const uint32_t sc_wave = lds_addr(lds) + SC_BASE + 256 * wave;     // + slot * SC_SLOT_B
+  uint32_t lane_k8 = 0, lane_v8 = 0;
+  auto seg_offsets8 = [&]() {
+    lane_k8 = (uint32_t)row8 * cs.ks + kcol8;
+    lane_v8 = (uint32_t)row8 * cs.vs + 16 * j8;
+  };
+  auto row8_clamped = [&](int rows) {
+    const int tvlo = rows & 0xff, rhi = ((rows >> 8) & 0xff) - 1;
+    return row8 < tvlo ? tvlo : (row8 > rhi ? rhi : row8);
+  };
+  // V codes and scales of the cursor's tile into staging slot `slot` (2 copies per lane)
+  auto issue_raw = [&](int slot) -> int {
     const int rows = cs.rows;
-    const int tvlo = rows & 0xff, tvhi = (rows >> 8) & 0xff;
-    int r = row8;
-    r = r < tvlo ? tvlo : (r > tvhi - 1 ? tvhi - 1 : r);
-    k8 = *reinterpret_cast<const u32x4*>(cs.kt + (uint32_t)r * cs.ks + 16 * j8);
-    v8 = *reinterpret_cast<const u32x4*>(cs.vt + (uint32_t)r * cs.vs + 16 * j8);
-    sk_n = *cs.ksc;
-    sv_n = *cs.vsc;
-    cursor_next<1>(a, lo, hi, b, h, mult, cs);
+    uint32_t voff = lane_v8;
+    if ((rows & 0xffff) != (BN << 8)) voff = (uint32_t)row8_clamped(rows) * cs.vs + 16 * j8;
+    dma16(cs.vt, voff, (uint32_t)sreg((int)raw_wave) + slot * TILE8_B);
+    const uint64_t sp = (lane & 1) ? (uint64_t)(uintptr_t)cs.vsc : (uint64_t)(uintptr_t)cs.ksc;
+    dma4(sp, (uint32_t)sreg((int)sc_wave) + slot * SC_SLOT_B);
     return rows;
   };
-  auto write8 = [&](int stage) {
-    auto cvt = [](const u32x4& x, int half) {
-      const uint32_t w0 = x[2 * half], w1 = x[2 * half + 1];
-      return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
-                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
-                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
-                   __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
-    };
-    unsigned char* kd = lds + stage * TILE_B + row8 * ROWB;
-    unsigned char* vd = kd + V_BASE;
+  // K codes of the cursor's tile into stage `stage` (1 copy per lane); then the cursor advances
+  auto issue_k8 = [&](int stage) {
+    const int rows = cs.rows;
+    uint32_t koff8 = lane_k8;
+    if ((rows & 0xffff) != (BN << 8)) koff8 = (uint32_t)row8_clamped(rows) * cs.ks + kcol8;
+    dma16(cs.kt, koff8, (uint32_t)sreg(lds0) + stage * TILE8_B + 1024 * wave);
+    if (cursor_next<1>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets8();
+  };
+  // this lane's 16 staged V codes of slot `slot` -> bf16 into V stage `stage` (row row8, logical
+  // chunks 2 j8 and 2 j8 + 1); the tile's block scales -> sk, sv
+  auto convert_v = [&](int slot, int stage, float& sk, float& sv) {
+    const u32x4 x = lds_read_b128((int)raw_wave + slot * TILE8_B + 16 * lane);
+    const u32x2 sc = lds_read_b64((int)sc_wave + slot * SC_SLOT_B);
+    unsigned char* vd = lds + V_BASE + stage * TILE_B + row8 * ROWB;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const int pc = ((2 * j8 + hf) ^ swz(row8)) << 4;
-      *reinterpret_cast<u32x4*>(kd + pc) = cvt(k8, hf);
-      *reinterpret_cast<u32x4*>(vd + pc) = cvt(v8, hf);
+      const uint32_t w0 = x[2 * hf], w1 = x[2 * hf + 1];
+      const u32x4 y = {
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+      *reinterpret_cast<u32x4*>(vd + (((2 * j8 + hf) ^ swz(row8)) << 4)) = y;
     }
+    sk = __uint_as_float(sc[0]);
+    sv = __uint_as_float(sc[1]);
   };
 
   const int T = t1 - t0;
@@ -296,15 +402,17 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     float skr[NSTAGE], svr[NSTAGE];  // fp8 block scales of the same tiles
 #pragma unroll
     for (int k = 0; k < NSTAGE; ++k) { vr[k] = ROWS_FULL; skr[k] = 1.0f; svr[k] = 1.0f; }
+    i32x8 qh[2], ql[2];  // fp8: the query operands (hi, lo) of d-halves 0 and 1
+    int sbh = 127, sbl = 127;  // and their e8m0 scales
     cursor_init<ESZ>(a, lo, hi, t0, b, h, cs);
     if constexpr (FP8) {
+      // tiles 0 and 1: staged V (slots 0, 1) and K (stages 0, 1)
+      seg_offsets8();
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k)
         if (k < T) {
-          vr[k] = issue8();
-          skr[k] = sk_n;
-          svr[k] = sv_n;
-          write8(k);
+          vr[k] = issue_raw(k);
+          issue_k8(k);
         }
     } else {
       seg_offsets();
@@ -323,7 +431,13 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     // of them, explicitly and on every path, so that the compiler, which cannot see the asm
     // K/V copies, does not re-wait for all memory before the first MFMA of every iteration
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero fill (and fp8 tiles) are done
+    if constexpr (FP8) {
+      // tile 0's V into stage 0 (read from the end of step 0 on), and the fp8 query operands
+      convert_v(0, 0, skr[0], svr[0]);
+      sbh = q8_split(qf, qh, ql);
+      sbl = sbh - 4;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the zero fill (and fp8 V tile) are done
     barrier_nofence();
 
     // Pipeline registers, double-buffered so that consecutive steps swap roles instead of
@@ -344,9 +458,19 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     constexpr int KR = K_AHEAD + 2, VR = V_AHEAD + 2;
     static_assert(8 % KR == 0 && 8 % VR == 0, "fragment rings must divide 8");
     u32x4 kf[KR], vf[VR];
+    i32x8 k8f[2];  // fp8: the K operands of d-halves 0 and 1
     auto load_k = [&](auto ko_c, int i) {
       constexpr int KO = decltype(ko_c)::value;
-      kf[i % KR] = lds_read_b128(koff[i] + KO);
+      if constexpr (FP8) {
+        const u32x4 x0 = lds_read_b128(koff[2 * i] + KO), x1 = lds_read_b128(koff[2 * i + 1] + KO);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          k8f[i][j] = (int)x0[j];
+          k8f[i][j + 4] = (int)x1[j];
+        }
+      } else {
+        kf[i % KR] = lds_read_b128(koff[i] + KO);
+      }
     };
     auto load_v = [&](auto vo_c, int i) {
       constexpr int VO = decltype(vo_c)::value;
@@ -359,10 +483,20 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     // S of sub-block 0 (tile 0, rows 0..31), and the first fragments of step 0: K of tile 0
     // rows 32..63, V of the zeroed "previous sub-block"
     if (wave_active) {
+      if constexpr (FP8) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
+        for (int m = 0; m < 2; ++m) {
+          load_k(std::integral_constant<int, 0>{}, m);
+          sA = mfma_qk8(k8f[m], qh[m], sA, sbh);
+          sA = mfma_qk8(k8f[m], ql[m], sA, sbl);
+        }
+        load_k(std::integral_constant<int, HALF8_B>{}, 0);
+      } else {
 #pragma unroll
-      for (int i = 0; i < K_AHEAD; ++i) load_k(std::integral_constant<int, HALF_B>{}, i);
+        for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
+#pragma unroll
+        for (int i = 0; i < K_AHEAD; ++i) load_k(std::integral_constant<int, HALF_B>{}, i);
+      }
 #pragma unroll
       for (int i = 0; i < V_AHEAD; ++i)
         load_v(std::integral_constant<int, (NSTAGE - 1) * TILE_B + HALF_B>{}, i);
@@ -378,8 +512,12 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       constexpr bool KPRE = decltype(kpre_c)::value, VPRE = decltype(vpre_c)::value;
       constexpr int NKO = decltype(nko_c)::value, NVO = decltype(nvo_c)::value;
       if constexpr (!KPRE) {
+        if constexpr (FP8) {
+          load_k(koff_c, 0);
+        } else {
 #pragma unroll
-        for (int i = 0; i < K_AHEAD; ++i) load_k(koff_c, i);
+          for (int i = 0; i < K_AHEAD; ++i) load_k(koff_c, i);
+        }
       }
       if constexpr (!VPRE) {
 #pragma unroll
@@ -430,11 +568,27 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        if (i + K_AHEAD < 8) load_k(koff_c, i + K_AHEAD);
-        else if constexpr (NKO >= 0) load_k(nko_c, i + K_AHEAD - 8);
+        if constexpr (FP8) {
+          // K of d-half 1 at once; the next step's d-half 0 once this step's last use of it
+          // (the lo product at i = 2) is issued
+          if (i == 0) load_k(koff_c, 1);
+          if constexpr (NKO >= 0)
+            if (i == 4) load_k(nko_c, 0);
+        } else {
+          if (i + K_AHEAD < 8) load_k(koff_c, i + K_AHEAD);
+          else if constexpr (NKO >= 0) load_k(nko_c, i + K_AHEAD - 8);
+        }
         if (i + V_AHEAD < 8) load_v(voff_c, i + V_AHEAD);
         else if constexpr (NVO >= 0) load_v(nvo_c, i + V_AHEAD - 8);
-        s_out = mfma32x32x16(kf[i % KR], qf[i], s_out);
+        if constexpr (FP8) {
+          // QK on the fp8 cores at even i: (d-half i / 4) x (hi, lo)
+          if ((i & 1) == 0) {
+            const int m = i >> 2;
+            s_out = (i & 2) ? mfma_qk8(k8f[m], ql[m], s_out, sbl) : mfma_qk8(k8f[m], qh[m], s_out, sbh);
+          }
+        } else {
+          s_out = mfma32x32x16(kf[i % KR], qf[i], s_out);
+        }
         oacc[i >> 1] = mfma32x32x16(vf[i % VR], p_in[i & 1], oacc[i >> 1]);
       }
       // softmax, part 2: P packed to bf16 in the PV operand order, fp32 row sum
@@ -460,11 +614,25 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       // reads of the pair K_AHEAD / V_AHEAD ahead, MFMA, 2 VALU; the rest of the VALU work is
       // left to the compiler. Measured against the compiler's own order and against 1, 3 or 4
       // VALU per MFMA and other places for the reads: 3.5 % faster than the next best.
-      constexpr int NDS0 = (KPRE ? 0 : K_AHEAD) + (VPRE ? 0 : 2 * V_AHEAD);
+      constexpr int NDS0 = (KPRE ? 0 : (FP8 ? 2 : K_AHEAD)) + (VPRE ? 0 : 2 * V_AHEAD);
       if constexpr (NDS0 > 0) __builtin_amdgcn_sched_group_barrier(0x100, NDS0, 0);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const bool rk = i + K_AHEAD < 8 || NKO >= 0, rv = i + V_AHEAD < 8 || NVO >= 0;
+        if constexpr (FP8) {
+          // the QK product (even i) and the PV product, 2 VALU after each, and between them
+          // the LDS reads: K operands at i = 0 and 4, V fragments V_AHEAD pairs ahead
+          const int nds = ((i == 0 || (i == 4 && NKO >= 0)) ? 2 : 0) + (rv ? 2 : 0);
+          if (i % 2 == 0) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          }
+          if (nds == 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+          else if (nds == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          continue;
+        }
         if constexpr (FOLD) {
           // (the VALU class does not take the exponentials, which without the FMAs would
           // otherwise bunch at the start of the step: one per MFMA, named as transcendentals)
@@ -487,6 +655,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
         }
       }
+      // fp8: the next sub-block's S is finished in this block as well (the compiler would
+      // otherwise sink its MFMA chain, used only by the next step, past the redo branch, where
+      // the dependent MFMAs issue back to back)
+      if constexpr (FP8) asm volatile("" ::"v"(s_out));
       if constexpr (FOLD) {
         asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(ls));
         // s_in is s - mref. Redo as below, and also while a row's reference is not yet set
@@ -550,6 +722,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     // Step 2u+1: softmax of tile u half 1, PV of tile u half 0, S of tile u+1 half 0.
     // Between them: wait for tile u+1, barrier (every wave is past its reads of tile u-1),
     // refill tile u-1's stage with tile u+NSTAGE-1.
+    // K tile bytes in LDS (bf16 16 KB, fp8 8 KB) and one sub-block's
+    constexpr int KT_B = FP8 ? TILE8_B : TILE_B, KH_B = KT_B / 2;
     auto tile = [&](auto st_c, int u) {
       constexpr int ST = decltype(st_c)::value;
       constexpr int SP = (ST + NSTAGE - 1) % NSTAGE;  // stage of tile u-1
@@ -557,36 +731,39 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       const int vrow = vr[0];
       const float sk = skr[0], sv = svr[0];
       if constexpr (FP8) {
-        // tile u+1 (loaded one tile ago) into its stage, the one tile u-2 left: free since the
-        // last barrier and not read before the next one, so the writes can overlap step 2u
-        if (u >= 1 && u + 1 < T) write8(SN);
+        // Copies in flight per lane, in issue order: staged V of tile u+1 (2, issued at the
+        // start of tile u-1), K of tile u+1 (1, after tile u-1's barrier). Tile u+1's V goes
+        // into its stage, the one tile u-2 left: free since the last barrier and not read
+        // before the next one. Then tile u+2's V and scales into the slot tile u's left.
+        if (u + 1 < T) {
+          wait_vm(1);
+          convert_v((u + 1) & 1, SN, skr[1], svr[1]);
+        }
+        if (u + 2 < T) vr[2] = issue_raw(u & 1);
       }
       // step 2u reads the V fragments of step 2u+1 (tile u, already resident); step 2u+1 reads
       // those of step 2u+2 (tile u+1 rows 32..63, resident since the barrier, and tile u)
       if (wave_active)
-        step(std::integral_constant<int, ST * TILE_B + HALF_B>{},
+        step(std::integral_constant<int, ST * KT_B + KH_B>{},
              std::integral_constant<int, SP * TILE_B + HALF_B>{}, std::true_type{},
              std::true_type{}, std::integral_constant<int, -1>{},
              std::integral_constant<int, ST * TILE_B>{}, sA, sB, pA, pB, 0, vrow, sk, sv);
       if constexpr (FP8) {
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the LDS writes are done
+        if (u + 1 < T) wait_vm(u + 2 < T ? 2 : 0);  // tile u+1's K (tile u+2's V may be in flight)
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V conversion's writes are done
       } else {
         if (u + 1 < T) wait_tiles_outstanding(min(NSTAGE - 3, T - 2 - u));
       }
       barrier_nofence();
       if constexpr (FP8) {
-        if (u + 2 < T) {
-          vr[2] = issue8();
-          skr[2] = sk_n;
-          svr[2] = sv_n;
-        }
+        if (u + 2 < T) issue_k8(SP);
       } else {
         if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = issue(SP);
       }
       if (wave_active)
-        step(std::integral_constant<int, SN * TILE_B>{},
+        step(std::integral_constant<int, SN * KT_B>{},
              std::integral_constant<int, ST * TILE_B>{}, std::false_type{}, std::true_type{},
-             std::integral_constant<int, SN * TILE_B + HALF_B>{},
+             std::integral_constant<int, SN * KT_B + KH_B>{},
              std::integral_constant<int, ST * TILE_B + HALF_B>{}, sB, sA, pB, pA, 1, vrow, sk, sv);
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k) {

@@ -26,6 +26,7 @@ typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) shortx4 lds_shortx4;
 
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 
 // LDS reads at an integer LDS byte address, so the constant part of an address folds into the
 // instruction's offset field.
@@ -36,6 +37,9 @@ __device__ __forceinline__ u32x2 lds_read_tr16(int addr) {
 __device__ __forceinline__ u32x4 lds_read_b128(int addr) {
   return *(const lds_u32x4*)(uintptr_t)addr;
 }
+__device__ __forceinline__ u32x2 lds_read_b64(int addr) {
+  return *(const lds_u32x2*)(uintptr_t)addr;
+}
 
 // 16 bytes per lane HBM -> LDS (global_load_lds_dwordx4): lane l's bytes from sbase + voff land
 // at LDS byte address lds_dst + 16 l. Inline asm rather than the builtin: the compiler's wait
@@ -44,6 +48,11 @@ __device__ __forceinline__ u32x4 lds_read_b128(int addr) {
 // for the tiles it reads itself (wait_tiles_outstanding, then a barrier).
 __device__ __forceinline__ void dma16(const unsigned char* sbase, uint32_t voff, uint32_t lds_dst) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_dst) : "memory");
+}
+// 4 bytes per lane from a per-lane 64-bit address (global_load_lds_dword): lane l's dword lands
+// at LDS byte address lds_dst + 4 l.
+__device__ __forceinline__ void dma4(uint64_t addr, uint32_t lds_dst) {
+  asm volatile("global_load_lds_dword %0, off" ::"v"(addr), "{m0}"(lds_dst) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {

@@ -50,11 +50,12 @@ def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softma
                     out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """Attention of bf16 q ``[B, Lq, N, 128]`` over fp8 segments ``[(Fp8KV k, Fp8KV v), ...]``.
 
-    The kernel converts each 64-token tile's codes exactly to bf16 on their way to LDS (every
-    e4m3 value is a bf16 value) and runs the bf16 MFMA loop with q unquantised; the K block
-    scale folds into the softmax exponent's multiplier and the V block scale into its addend
-    (and out of the row sum). ``out_dtype=torch.float32`` returns the output before its bf16
-    rounding."""
+    Q K^T runs on the fp8 matrix cores: the K codes go to LDS as they are, and each query is
+    split into two e4m3 operands (hi + lo / 16, times a power of two per query) that hold its
+    bf16 values. The V codes are converted exactly to bf16 (every e4m3 value is a bf16 value) and
+    P V runs on the bf16 matrix cores. The K block scale folds into the softmax exponent's
+    multiplier and the V block scale into its addend (and out of the row sum).
+    ``out_dtype=torch.float32`` returns the output before its bf16 rounding."""
     ops = _lib.ops()
     device = q.device
     _check_4d("q", q, device)

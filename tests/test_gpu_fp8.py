@@ -108,3 +108,107 @@ def test_fp8_full_size_long_horizon(lib):
         c = cosine(out[:, sel, h:h + 1], ref)
         print(f"fp8 full size head {h}: cosine {c:.6f}")
         assert c >= FP8_COSINE
+
+
+def _wide_q(Lq, H, g):
+    """q rows with magnitudes 2^-12 .. 2^2, row 0 all zero (uniform weights) and row 1 a
+    single nonzero element: the per-query exponent of the fp8 query operands at its edges."""
+    q = torch.randn(1, Lq, H, 128, generator=g)
+    q = q * torch.exp2(torch.randint(-12, 3, (1, Lq, H, 1), generator=g).float())
+    q[0, 0] = 0.0
+    if Lq > 1:
+        q[0, 1] = 0.0
+        q[0, 1, :, 77] = 3.0
+    return q.to(torch.bfloat16)
+
+
+# The fp8 matrix cores sum each group of 8 consecutive products of an x64 MFMA in fixed point
+# aligned to the group's largest product, dropping the bits more than 2^12 below it (measured on
+# structured sums); the group sums then add in fp32. With the query split into hi and lo
+# operands that hold its bf16 values, a score's error is below 7 * 2^-12 * (1 + 2^-4) per
+# group's largest |q_d k_d|, i.e. below 2^-9 sum_d |q_d k_d|.
+def _score_err(q, kd, scale):
+    """Per query row: 2^-9 * scale * max over keys of sum_d |q_d k_d| ([B, Lq, H])."""
+    qa, ka = q.float().abs(), kd.float().abs()
+    s = torch.einsum("blhd,bkhd->blhk", qa, ka).amax(-1)
+    return s * scale * 2.0 ** -9
+
+
+def _row_bound(vd, delta):
+    """|o - o_ref| per row: P's bf16 rounding (2^-8 max|V|) plus weights off by at most
+    e^(2 delta) - 1 in total from the score errors."""
+    return float(vd.abs().max()) * (2.0 ** -8 * 1.01 + torch.expm1(2 * delta)) + 1e-5
+
+
+@pytest.mark.parametrize("Lq,H,lk,window,splits", [
+    (1, 1, 1, None, 0),              # one key: a single partial tile
+    (33, 2, 64, None, 0),            # exactly one tile
+    (100, 2, 65, None, 0),           # a tile and one row
+    (257, 3, 130, (3, 129), 0),      # partial first and last tiles, a partial wave
+    (300, 2, 2000, None, 1),
+    (300, 2, 2000, None, 3),         # split-KV partials and their merge
+    (64, 5, 4096, (1000, 3001), 0),
+])
+def test_fp8_kernel_arithmetic_fp32(lib, Lq, H, lk, window, splits):
+    """The kernel against the oracle run on the dequantised K/V, on the fp32 output, row by row
+    within the bound its arithmetic fixes (P rounded to bf16, the fp8 cores' score error); and
+    the relative L1 error against the same oracle stays at the level of P's bf16 rounding."""
+    from lbw_amd import attention_fp8kv, quantize_kv_fp8
+    g = torch.Generator().manual_seed(lk + Lq)
+    q = _wide_q(Lq, H, g)
+    k = _outliers(torch.randn(1, lk, H, 128, generator=g), g).to(torch.bfloat16)
+    v = _outliers(torch.randn(1, lk, H, 128, generator=g), g).to(torch.bfloat16)
+    kq, vq = quantize_kv_fp8(k.to(DEV)), quantize_kv_fp8(v.to(DEV))
+    lo, hi = (None, None) if window is None else window
+    print(f"case Lq={Lq} H={H} lk={lk} window={window} splits={splits}", flush=True)
+    out = attention_fp8kv(q.to(DEV), [(kq, vq)], kv_lo=lo, kv_hi=hi, num_splits=splits,
+                          out_dtype=torch.float32)
+    kd = O.dequantize_kv_fp8(kq.codes.cpu(), kq.scales.cpu())
+    vd = O.dequantize_kv_fp8(vq.codes.cpu(), vq.scales.cpu())
+    ref = O.attention_ref(q, kd, vd, kv_lo=lo, kv_hi=hi)
+    a, b = (0, lk) if window is None else window
+    bound = _row_bound(vd[:, a:b], _score_err(q, kd[:, a:b], 128 ** -0.5))
+    err = (out.cpu() - ref).abs().amax(-1)
+    rel_l1 = float((out.cpu() - ref).abs().sum() / ref.abs().sum().clamp_min(1e-30))
+    print(f"  max err {float(err.max()):.3e} (row bound min {float(bound.min()):.3e}), "
+          f"rel_l1 {rel_l1:.3e}, worst err/bound {float((err / bound).max()):.3f}")
+    assert bool((err <= bound).all())
+    assert rel_l1 <= 4e-3
+
+
+def test_fp8_partials_capi_match_oracle(lib):
+    """The unnormalised partials (cte_partial contract: O and l relative to the row max m of the
+    scaled scores) of the fp8 entry point, called through the C ABI, against the oracle on the
+    dequantised K/V; two unaligned segments, a window. m within the score error bound, O / l
+    within the output bound, l within e^(2 delta) - 1 relative."""
+    from lbw_amd import _lib, quantize_kv_fp8
+    g = torch.Generator().manual_seed(7)
+    B, Lq, H = 1, 150, 2
+    segs, kds, vds = [], [], []
+    for L in (300, 190):
+        k = _outliers(torch.randn(B, L, H, 128, generator=g), g).to(torch.bfloat16)
+        v = _outliers(torch.randn(B, L, H, 128, generator=g), g).to(torch.bfloat16)
+        kq, vq = quantize_kv_fp8(k.to(DEV)), quantize_kv_fp8(v.to(DEV))
+        segs.append((kq.codes, vq.codes, kq.scales, vq.scales))
+        kds.append(O.dequantize_kv_fp8(kq.codes.cpu(), kq.scales.cpu()))
+        vds.append(O.dequantize_kv_fp8(vq.codes.cpu(), vq.scales.cpu()))
+    q = _wide_q(Lq, H, g)
+    qd = q.to(DEV)
+    po = torch.empty(B, H, Lq, 128, device=DEV)
+    pm = torch.empty(B, H, Lq, device=DEV)
+    pl = torch.empty(B, H, Lq, device=DEV)
+    p = _lib.attn_params(qd, None, segs, 40, 470, None, None, 0, parts=(po, pm, pl))
+    L = _lib.load()
+    ws_bytes = L.lbw_attention_fp8kv_workspace_size(p)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    _lib.check(L.lbw_attention_fwd_fp8kv(p, ws.data_ptr(), ws_bytes, _lib.stream_ptr(DEV)),
+               "lbw_attention_fwd_fp8kv")
+    torch.cuda.synchronize()
+    kd, vd = torch.cat(kds, 1)[:, 40:470], torch.cat(vds, 1)[:, 40:470]
+    _, (ro, rm, rl) = O.attention_ref(q, kd, vd, return_partials=True)
+    delta = _score_err(q, kd, 128 ** -0.5).permute(0, 2, 1)  # [B, H, Lq]
+    assert bool(((pm.cpu() - rm).abs() <= delta + 1e-5 * rm.abs() + 1e-6).all())
+    assert bool(((pl.cpu() - rl).abs() <= rl * (torch.expm1(2 * delta) + 1e-3)).all())
+    o, r = po.cpu() / pl.cpu()[..., None], ro / rl[..., None]
+    bound = _row_bound(vd, delta)[..., None]
+    assert bool(((o - r).abs() <= bound).all())
