@@ -340,23 +340,27 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     return rows;
   };
 
-  // fp8: thread t (= 64 wave + lane) copies 16-byte code chunk t % 8 of a row of each tile:
-  // K codes of row t / 8 into the K tile (at physical chunk t % 8, so the logical chunk is
-  // (t % 8) ^ swz8), V codes of row vrow8 into its wave's staging slot (at 16 lane), and lanes
-  // 0 / 1 copy the K / V block scale (dwords 0 and 1 of the wave's scale slot). Rows outside a partial tile's valid range
-  // fetch a valid row instead, as above. The copying wave converts its own staged V rows.
+  // fp8: per tile, thread t (= 64 wave + lane) copies the K codes of row t / 8 into the K tile
+  // (at physical chunk t % 8, so the logical chunk is (t % 8) ^ swz8) and the 16 V codes of
+  // row vrow8, chunk vj8 into its wave's staging slot (at 16 lane); lanes 0 / 1 copy the K / V
+  // block scale (dwords 0 and 1 of the wave's scale slot). Rows outside a partial tile's valid
+  // range fetch a valid row instead, as above. The copying wave converts its own staged V.
   const int row8 = threadIdx.x >> 3, j8 = threadIdx.x & 7;
   const int kcol8 = (j8 ^ swz8(row8)) << 4;
-  // The V rows go the other way round: lanes 8-15 of every 16 take the rows 4 below those of
-  // lanes 0-7, whose swizzles differ in parity, so that each 16 lanes' bf16 writes of the
-  // conversion cover the 64 LDS banks once (adjacent rows would hit every bank twice).
-  const int vrow8 = 8 * wave + ((lane >> 4) & 3) + 4 * ((lane >> 3) & 1);
+  // The V codes are mapped for the conversion's bf16 writes: a 16-byte LDS write serves 8
+  // lanes per clock over 32 banks (measured: SQ_LDS_BANK_CONFLICT is 0 only then), so each 8
+  // lanes must write 8 distinct chunks mod 8. A lane's 16 codes become two adjacent bf16 chunks
+  // (2 vj8, 2 vj8 + 1), which for 8 lanes of one row cover only 4 residues; so each group of 8
+  // lanes takes half-rows of two rows 4 apart, whose swizzles differ in parity: row
+  // (g & 3) + 4 (u / 4), chunk pair (u & 3) + 4 (g / 4) for lane 8 g + u.
+  const int vrow8 = 8 * wave + ((lane >> 3) & 3) + 4 * ((lane >> 2) & 1);
+  const int vj8 = (lane & 3) + 4 * (lane >> 5);
   const uint32_t raw_wave = lds_addr(lds) + RAW_BASE + 1024 * wave;  // + slot * TILE8_B
   const uint32_t sc_wave = lds_addr(lds) + SC_BASE + 256 * wave;     // + slot * SC_SLOT_B
   uint32_t lane_k8 = 0, lane_v8 = 0;
   auto seg_offsets8 = [&]() {
     lane_k8 = (uint32_t)row8 * cs.ks + kcol8;
-    lane_v8 = (uint32_t)vrow8 * cs.vs + 16 * j8;
+    lane_v8 = (uint32_t)vrow8 * cs.vs + 16 * vj8;
   };
   auto clamped = [](int r, int rows) {
     const int tvlo = rows & 0xff, rhi = ((rows >> 8) & 0xff) - 1;
@@ -366,7 +370,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   auto issue_raw = [&](int slot) -> int {
     const int rows = cs.rows;
     uint32_t voff = lane_v8;
-    if ((rows & 0xffff) != (BN << 8)) voff = (uint32_t)clamped(vrow8, rows) * cs.vs + 16 * j8;
+    if ((rows & 0xffff) != (BN << 8)) voff = (uint32_t)clamped(vrow8, rows) * cs.vs + 16 * vj8;
     dma16(cs.vt, voff, (uint32_t)sreg((int)raw_wave) + slot * TILE8_B);
     const uint64_t sp = (lane & 1) ? (uint64_t)(uintptr_t)cs.vsc : (uint64_t)(uintptr_t)cs.ksc;
     dma4(sp, (uint32_t)sreg((int)sc_wave) + slot * SC_SLOT_B);
@@ -381,7 +385,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     if (cursor_next<1>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets8();
   };
   // this lane's 16 staged V codes of slot `slot` -> bf16 into V stage `stage` (row vrow8,
-  // logical chunks 2 j8 and 2 j8 + 1); the tile's block scales -> sk, sv
+  // logical chunks 2 vj8 and 2 vj8 + 1); the tile's block scales -> sk, sv
   auto convert_v = [&](int slot, int stage, float& sk, float& sv) {
     const u32x4 x = lds_read_b128((int)raw_wave + slot * TILE8_B + 16 * lane);
     const u32x2 sc = lds_read_b64((int)sc_wave + slot * SC_SLOT_B);
@@ -394,7 +398,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
           __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
           __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
-      *reinterpret_cast<u32x4*>(vd + (((2 * j8 + hf) ^ swz(vrow8)) << 4)) = y;
+      *reinterpret_cast<u32x4*>(vd + (((2 * vj8 + hf) ^ swz(vrow8)) << 4)) = y;
     }
     sk = __uint_as_float(sc[0]);
     sv = __uint_as_float(sc[1]);
