@@ -139,6 +139,8 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
   };
   u32x4 qf[8], qn[8];
   load_q(r0, qf);
+  int kl_b = -1;            // the batch whose valid key count kl_v holds
+  int64_t kl_v = 0;
 
 #pragma unroll 1
   for (int r = r0; r < r1; ++r) {
@@ -147,8 +149,11 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
     load_q(r + 1, qn);
     int64_t hi = a.hi;
     if (a.k_lens != nullptr) {
-      const int64_t kl = load_scalar_i32(a.k_lens + b);
-      hi = kl < hi ? kl : hi;
+      if (b != kl_b) {  // (a scalar round trip, so only when the batch changes)
+        kl_v = load_scalar_i32(a.k_lens + b);
+        kl_b = b;
+      }
+      hi = kl_v < hi ? kl_v : hi;
     }
     const int n_all = hi > lo ? (int)(hi - lo) : 0;  // attended keys (<= 4096, host-checked)
     const int nch = (n_all + XCH - 1) / XCH;
@@ -238,6 +243,17 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
         }
         if (pend) scale_acc(oacc, alpha_p);
         if (32 * J + 32 > n || mrow < 32 * J + 32) mask_scores(s_in, J, 0, n, hl, mrow, mult_raw);
+        if constexpr (J == 0) {
+          // a round's first sub-block: O and l are still 0, so the reference is set to the
+          // sub-block's row max directly (key 0 is valid, so it is finite) instead of starting
+          // at M_INIT, overflowing and redoing the exponentials
+          if (ch == 0) {
+            float mx = s_in[0];
+#pragma unroll
+            for (int e = 1; e < 16; ++e) mx = fmaxf(mx, s_in[e]);
+            m_used = wave_max_xor32(mx);
+          }
+        }
         float ca = -m_used * c;
         if constexpr (NEXT) {
 #pragma unroll
