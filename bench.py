@@ -157,9 +157,11 @@ def _gpu_busy(ms: float):
     torch.cuda._sleep(int(_SLEEP_CYCLES_PER_MS[0] * ms))
 
 
-def _time_ms(fn, iters=10, warmup=2):
-    """GPU time per call of ``fn``. The GPU is kept busy while the host queues the timed calls,
-    so that the Python/ctypes time between launches of a short kernel is not counted."""
+def _time_ms(fn, iters=10, warmup=2, reps=5):
+    """GPU time per call of ``fn``: the median over ``reps`` repetitions of ``iters`` calls back
+    to back (single 10-call averages of one shape spread by 5-10 % from one repetition to the
+    next). The GPU is kept busy while the host queues each repetition's calls, so that the
+    Python/ctypes time between launches of a short kernel is not counted."""
     import torch
     host_ms = 1.0
     for _ in range(max(warmup, 2)):
@@ -169,13 +171,17 @@ def _time_ms(fn, iters=10, warmup=2):
         host_ms = (time.perf_counter() - t0) * 1e3   # host time of one launch (the last one)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    _gpu_busy(min(2.0 + 2.0 * host_ms * iters, 500.0))
-    e0.record()
-    for _ in range(iters):
-        fn()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / iters
+    per_call = []
+    for _ in range(reps):
+        _gpu_busy(min(2.0 + 2.0 * host_ms * iters, 500.0))
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        per_call.append(e0.elapsed_time(e1) / iters)
+    per_call.sort()
+    return per_call[len(per_call) // 2]
 
 
 def other_configs(dev):
@@ -192,7 +198,8 @@ def other_configs(dev):
                             ("wan14b_480p_3f_over_18f", 40, 4680, 28080)):
         q = rnd(1, lq, h, D)
         kc, vc, kn, vn = rnd(1, lc, h, D), rnd(1, lc, h, D), rnd(1, lq, h, D), rnd(1, lq, h, D)
-        ms = _time_ms(lambda: attention_segments(q, [(kc, vc), (kn, vn)]))
+        o = torch.empty_like(q)
+        ms = _time_ms(lambda: attention_segments(q, [(kc, vc), (kn, vn)], out=o))
         fl = 4.0 * lq * (lc + lq) * D * h
         out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
                      "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2)}
@@ -217,7 +224,8 @@ def other_configs(dev):
     lk = 3600 * 25
     k8 = quantize_kv_fp8(rnd(1, lk, 40, D))
     v8 = quantize_kv_fp8(rnd(1, lk, 40, D))
-    ms = _time_ms(lambda: attention_fp8kv(q, [(k8, v8)]))
+    o = torch.empty_like(q)
+    ms = _time_ms(lambda: attention_fp8kv(q, [(k8, v8)], out=o))
     fl = 4.0 * 3600 * lk * D * 40
     out["wan14b_720p_1f_over_24f_fp8kv"] = {
         "ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
