@@ -121,7 +121,9 @@ int lbw_attention_fwd(const lbw_attn_params* p, void* workspace, size_t workspac
 int lbw_attention_fwd_noalloc(const lbw_attn_params* p, void* stream);
 
 /* Cross-attention to a short context (one segment of <= 4096 keys, typically 512), with the
- * optional per-batch valid length p->k_lens. Single pass, no workspace. */
+ * optional per-batch valid length p->k_lens. Single pass, no workspace. Up to 320 attended keys
+ * stay resident in LDS per (batch, head) (the masked 300-row context); longer unmasked contexts
+ * run the chunk kernel as a single pass. */
 int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream);
 
 /* Exact deduplicated cross-attention (no mask): keys n_distinct .. len-1 of the one segment
@@ -132,7 +134,8 @@ int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream);
 int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, void* stream);
 
 /* fp8-e4m3 KV cache: K/V segments hold e4m3fn codes with per-(batch, head, 64-token block)
- * fp32 scales (lbw_kv_quant_fp8's layout); Q stays bf16. */
+ * fp32 scales (lbw_kv_quant_fp8's layout); Q is given in bf16. Q K^T runs on the fp8 matrix
+ * cores (each query split into two e4m3 operands that hold its bf16 values), P V in bf16. */
 int lbw_attention_fwd_fp8kv(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
                             void* stream);
 
