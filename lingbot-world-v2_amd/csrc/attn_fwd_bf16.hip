@@ -450,8 +450,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
     // Pipeline registers, double-buffered so that consecutive steps swap roles instead of
     // copying: S of the sub-block being softmaxed / being computed, P of the previous / current
-    // sub-block. `pend` / `alpha_p`: an O rescale decided by the previous step, applied at the
-    // start of the next one (after the PV MFMAs that still used the old reference).
+    // sub-block. `pend` / `alpha_p` (TRACK): an O rescale decided at the start of the previous
+    // step, applied at the start of the next one (after the PV MFMAs that still used the old
+    // reference). The other forms decide a move after the step's MFMAs and rescale O right in
+    // the redo branch, so the common path carries no rescale branch.
     floatx16 sA, sB, cinit;  // cinit (FOLD): -mref, the start of every QK chain
 #pragma unroll
     for (int r = 0; r < 16; ++r) { sA[r] = 0.0f; sB[r] = 0.0f; cinit[r] = 0.0f; }
@@ -531,7 +533,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 #pragma unroll
         for (int i = 0; i < V_AHEAD; ++i) load_v(voff_c, i);
       }
-      if (pend) scale_acc(oacc, alpha_p);
+      if constexpr (TRACK) {
+        if (pend) scale_acc(oacc, alpha_p);
+      }
       const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
       if (vrow != ROWS_FULL && (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32))
         mask_scores(s_in, kb, vlo, vhi, hl, mrow, mult_raw);
@@ -681,6 +685,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           if (mlim > 0.0f) {
             d = fmaxf(mx, 0.0f);
             alpha = fast_exp2(-d);
+            // O (with this step's PV of the previous sub-block, at the old reference) moves now
+            scale_acc(oacc, alpha);
           } else {
             const bool set = mx > -INFINITY;  // a fully masked sub-block leaves it unset
             d = set ? mx : 0.0f;
@@ -715,13 +721,15 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           m_used = m_new;
           move = true;
           ca = lsv - m_new * c;
+          // O (with this step's PV of the previous sub-block, at the old reference) moves now
+          scale_acc(oacc, alpha);
           ls = exps();
         }
       }
       lsum = __builtin_fmaf(lsum, alpha, ls);
       // keep the exponentials in this step's block (not sunk into the next one)
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
-      pend = move;
+      pend = TRACK && move;  // (the other forms have rescaled O in the redo branch)
       alpha_p = alpha;
     };
 
