@@ -211,8 +211,6 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
       floatx16 sA, sB;
       u32x4 pA[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
       u32x4 pB[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-      bool pend = false;
-      float alpha_p = 1.0f;
       u32x4 kf[XKR], vf[XVR];
 #pragma unroll
       for (int e = 0; e < 16; ++e) { sA[e] = 0.0f; sB[e] = 0.0f; }
@@ -241,7 +239,6 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
             vb[db][1] = opaque(vb[db][1] + XSHIFT);
           }
         }
-        if (pend) scale_acc(oacc, alpha_p);
         if (32 * J + 32 > n || mrow < 32 * J + 32) mask_scores(s_in, J, 0, n, hl, mrow, mult_raw);
         if constexpr (J == 0) {
           // a round's first sub-block: O and l are still 0, so the reference is set to the
@@ -303,9 +300,15 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
           }
         }
         asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(ls));
+        // The next sub-block's S and the next step's first fragments stay in this step's block:
+        // they are used only if there is a next step, and the compiler would otherwise sink them
+        // into that step's branch, where the QK chain and its LDS reads then issue back to back
+        // ahead of the softmax instead of interleaved with it.
+        if constexpr (NEXT) asm volatile("" ::"v"(s_out));
+        asm volatile("" ::"v"(kf[0]), "v"(kf[1]), "v"(kf[2]), "v"(kf[3]));
+        asm volatile("" ::"v"(vf[0]), "v"(vf[1]), "v"(vf[2]), "v"(vf[3]));
         // a row sum beyond 2^16 (or not finite) means some p outgrew the reference: move it to
         // the row max of this sub-block (and the old reference), redo, and rescale O and l
-        bool move = false;
         float alpha = 1.0f;
         if (__any(!(ls <= P_LIMIT))) {
           float mx = s_in[0];
@@ -315,14 +318,13 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
           const float m_new = fmaxf(mx, m_used);
           alpha = fast_exp2((m_used - m_new) * c);
           m_used = m_new;
-          move = true;
           ca = -m_new * c;
+          // O (with this step's PV of the previous sub-block, at the old reference) moves now
+          scale_acc(oacc, alpha);
           ls = exps();
         }
         lsum = __builtin_fmaf(lsum, alpha, ls);
         asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
-        pend = move;
-        alpha_p = alpha;
       };
       auto run = [&](auto j_c, floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2],
                      u32x4 (&p_out)[2]) -> bool {
@@ -341,8 +343,6 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
       // drain: O += V_J^T P_J^T of the chunk's last sub-block J = nsub - 1 (P_J is in pA for
       // even J, pB for odd), with the V bases as step J left them
       {
-        if (pend) scale_acc(oacc, alpha_p);
-        pend = false;
         const int jl = nsub - 1;
         const int voff = (jl - (jl >= XVSW ? 5 : 0)) * XSUBB;
         u32x4 pl[2];
