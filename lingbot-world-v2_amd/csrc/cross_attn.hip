@@ -298,6 +298,14 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
           }
+        } else if constexpr (PV) {
+          // the tenth step: the 8 PV MFMAs, the V reads, the softmax spread between them
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          }
         }
         asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(ls));
         // The next sub-block's S and the next step's first fragments stay in this step's block:
@@ -329,10 +337,10 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
       auto run = [&](auto j_c, floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2],
                      u32x4 (&p_out)[2]) -> bool {
         constexpr int J = decltype(j_c)::value;
-        // (every step computes S_{J+1}: a last step without it, as a branch of its own, doubles
-        // the live ranges the register allocator sees and spills; the wasted MFMAs are 8 of the
-        // chunk's 8 + 16 nsub)
-        step(j_c, std::true_type{}, s_in, s_out, p_in, p_out);
+        // (every step but the chunk's tenth computes S_{J+1}, used if J + 1 < nsub: a last step
+        // without it as a branch of its own doubles the live ranges the register allocator sees
+        // and spills; a chunk of fewer than 10 sub-blocks wastes 8 of its 8 + 16 nsub MFMAs)
+        step(j_c, std::bool_constant<(J + 1 < XSB)>{}, s_in, s_out, p_in, p_out);
         return J + 1 < nsub;
       };
       static_assert(XSB == 10, "the unrolled sub-block sequence below covers 10 sub-blocks");
