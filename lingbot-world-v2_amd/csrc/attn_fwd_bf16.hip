@@ -180,10 +180,13 @@ __global__ void __launch_bounds__(64) attn_queue_reset_kernel(uint32_t* q) {
 // FOLD: scale * log2(e) == 1, i.e. q already carries log2(e)/sqrt(d) (a pre-scaled q, as the
 // fused q/k kernel writes it): the QK chain starts from -m instead of 0, so the MFMA result is
 // already the exponent of p and the softmax needs no per-score FMA (see the step).
-template <bool FP8, bool TRACK, bool FOLD>
+// SEG1: one KV segment and no multiplicity bias (a flat cache's window, bf16): the tile copies
+// are addressed by the tile index (see issue1) instead of walked by the general cursor.
+template <bool FP8, bool TRACK, bool FOLD, bool SEG1>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   static_assert(!FOLD || (!FP8 && !TRACK), "the folded softmax is the plain bf16 form");
+  static_assert(!SEG1 || !FP8, "the index-addressed copies are the bf16 form's");
   constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
@@ -339,6 +342,39 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     if (cursor_next<ESZ>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets();
     return rows;
   };
+  // SEG1: tile g of the walk is local tile g + s_lt0 of the one segment; its K/V rows come from
+  // the index, and only the segment's first and last tiles compute their valid rows. Nothing is
+  // carried from one copy to the next, so the tile loop's only state is its counter.
+  int s_lt0 = 0, s_first = 0, s_last = 0;
+  const unsigned char* s_kb = nullptr;  // local tile 0 of the segment, (b, h)
+  const unsigned char* s_vb = nullptr;
+  auto issue1 = [&](int stage, int g) -> int {
+    const int lt = g + s_lt0;
+    const unsigned char* kt = s_kb + (uint64_t)(uint32_t)lt * cs.kstep;
+    const unsigned char* vt = s_vb + (uint64_t)(uint32_t)lt * cs.vstep;
+    const uint32_t kdst = (uint32_t)sreg((int)lds_wave) + stage * TILE_B;
+    const uint32_t vdst = kdst + V_BASE;
+    if (lt > s_first && lt < s_last) {  // every row valid
+#pragma unroll
+      for (int i = 0; i < NDMA; ++i) {
+        dma16(kt, lane_k[i], kdst + 1024 * i);
+        dma16(vt, lane_v[i], vdst + 1024 * i);
+      }
+      return ROWS_FULL;
+    }
+    const int row0 = lt * BN;
+    const int l = cs.la - row0, u = cs.lb - row0;
+    const int tvlo = l > 0 ? l : 0, vhi = u < BN ? u : BN;
+    const int rhi = vhi - 1;
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      int r = dma_row[i];
+      r = r < tvlo ? tvlo : (r > rhi ? rhi : r);
+      dma16(kt, (uint32_t)r * cs.ks + dma_col[i], kdst + 1024 * i);
+      dma16(vt, (uint32_t)r * cs.vs + dma_col[i], vdst + 1024 * i);
+    }
+    return pack_rows(tvlo, vhi, 255);
+  };
 
   // fp8: per tile, thread t (= 64 wave + lane) copies the K codes of row t / 8 into the K tile
   // (at physical chunk t % 8, so the logical chunk is (t % 8) ^ swz8) and the 16 V codes of
@@ -424,9 +460,16 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         }
     } else {
       seg_offsets();
+      if constexpr (SEG1) {
+        s_lt0 = cs.lt;
+        s_first = cs.la / BN;
+        s_last = cs.lt_end - 1;
+        s_kb = cs.kt - (int64_t)cs.lt * cs.kstep;
+        s_vb = cs.vt - (int64_t)cs.lt * cs.vstep;
+      }
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k)
-        if (k < T) vr[k] = issue(k);
+        if (k < T) vr[k] = SEG1 ? issue1(k, k) : issue(k);
     }
     // The first step's "previous sub-block" is the second half of stage NSTAGE-1's V tile
     // with P = 0: zero it so that 0 * V stays 0 (that stage is only filled after barrier 0).
@@ -774,7 +817,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       if constexpr (FP8) {
         if (u + 2 < T) issue_k8(SP);
       } else {
-        if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = issue(SP);
+        if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = SEG1 ? issue1(SP, u + NSTAGE - 1) : issue(SP);
       }
       if (wave_active)
         step(std::integral_constant<int, SN * KT_B>{},
@@ -908,9 +951,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-template <bool FP8, bool TRACK, bool FOLD = false>
+template <bool FP8, bool TRACK, bool FOLD = false, bool SEG1 = false>
 static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD>,
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEG1>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t U = (uint32_t)a.n_qtiles * a.H * a.B;
@@ -922,15 +965,19 @@ static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
     nwg += 8u * ((per_xcd + 15u) / 16u);
     hipLaunchKernelGGL(attn_queue_reset_kernel, dim3(1), dim3(64), 0, stream, a.queue);
   }
-  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEG1>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
                      stream, a);
   return hipGetLastError();
 }
 
 hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
   if (a.track_max) return launch<false, true>(a, stream);
-  // a pre-scaled q (scale * log2(e) exactly 1 in fp32) takes the folded softmax
-  return a.scale_log2 == 1.0f ? launch<false, false, true>(a, stream) : launch<false, false>(a, stream);
+  // a pre-scaled q (scale * log2(e) exactly 1 in fp32) takes the folded softmax; one segment
+  // with no multiplicity bias the index-addressed tile copies
+  const bool seg1 = a.nseg == 1 && a.mult_key < 0;
+  if (a.scale_log2 == 1.0f)
+    return seg1 ? launch<false, false, true, true>(a, stream) : launch<false, false, true>(a, stream);
+  return seg1 ? launch<false, false, false, true>(a, stream) : launch<false, false>(a, stream);
 }
 
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {
