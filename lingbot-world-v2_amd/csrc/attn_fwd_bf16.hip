@@ -180,13 +180,13 @@ __global__ void __launch_bounds__(64) attn_queue_reset_kernel(uint32_t* q) {
 // FOLD: scale * log2(e) == 1, i.e. q already carries log2(e)/sqrt(d) (a pre-scaled q, as the
 // fused q/k kernel writes it): the QK chain starts from -m instead of 0, so the MFMA result is
 // already the exponent of p and the softmax needs no per-score FMA (see the step).
-// SEG1: one KV segment and no multiplicity bias (a flat cache's window, bf16): the tile copies
-// are addressed by the tile index (see issue1) instead of walked by the general cursor.
+// SEG1: one KV segment and no multiplicity bias (a flat cache's window): the tile copies are
+// addressed by the tile index (issue1, issue_raw1, issue_k81) instead of walked by the general
+// cursor.
 template <bool FP8, bool TRACK, bool FOLD, bool SEG1>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   static_assert(!FOLD || (!FP8 && !TRACK), "the folded softmax is the plain bf16 form");
-  static_assert(!SEG1 || !FP8, "the index-addressed copies are the bf16 form's");
   constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
@@ -348,6 +348,14 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   int s_lt0 = 0, s_first = 0, s_last = 0;
   const unsigned char* s_kb = nullptr;  // local tile 0 of the segment, (b, h)
   const unsigned char* s_vb = nullptr;
+  const float* s_ksc = nullptr;         // fp8: the block scales of local tile 0
+  const float* s_vsc = nullptr;
+  // packed valid rows of local tile lt at the segment's ends (no bias)
+  auto rows_at = [&](int lt) -> int {
+    const int row0 = lt * BN;
+    const int l = cs.la - row0, u = cs.lb - row0;
+    return pack_rows(l > 0 ? l : 0, u < BN ? u : BN, 255);
+  };
   auto issue1 = [&](int stage, int g) -> int {
     const int lt = g + s_lt0;
     const unsigned char* kt = s_kb + (uint64_t)(uint32_t)lt * cs.kstep;
@@ -362,10 +370,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
       return ROWS_FULL;
     }
-    const int row0 = lt * BN;
-    const int l = cs.la - row0, u = cs.lb - row0;
-    const int tvlo = l > 0 ? l : 0, vhi = u < BN ? u : BN;
-    const int rhi = vhi - 1;
+    const int rows = rows_at(lt);
+    const int tvlo = rows & 0xff, rhi = ((rows >> 8) & 0xff) - 1;
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       int r = dma_row[i];
@@ -373,7 +379,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       dma16(kt, (uint32_t)r * cs.ks + dma_col[i], kdst + 1024 * i);
       dma16(vt, (uint32_t)r * cs.vs + dma_col[i], vdst + 1024 * i);
     }
-    return pack_rows(tvlo, vhi, 255);
+    return rows;
   };
 
   // fp8: per tile, thread t (= 64 wave + lane) copies the K codes of row t / 8 into the K tile
@@ -420,6 +426,40 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     dma16(cs.kt, koff8, (uint32_t)sreg(lds0) + stage * TILE8_B + 1024 * wave);
     if (cursor_next<1>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets8();
   };
+  // SEG1 forms of the two: tile g of the walk, addressed by its index
+  auto issue_raw1 = [&](int slot, int g) -> int {
+    const int lt = g + s_lt0;
+    const unsigned char* vt = s_vb + (uint64_t)(uint32_t)lt * cs.vstep;
+    int rows = ROWS_FULL;
+    uint32_t voff = lane_v8;
+    if (!(lt > s_first && lt < s_last)) {
+      rows = rows_at(lt);
+      voff = (uint32_t)clamped(vrow8, rows) * cs.vs + 16 * vj8;
+    }
+    dma16(vt, voff, (uint32_t)sreg((int)raw_wave) + slot * TILE8_B);
+    const uint64_t sp = (lane & 1) ? (uint64_t)(uintptr_t)(s_vsc + lt) : (uint64_t)(uintptr_t)(s_ksc + lt);
+    dma4(sp, (uint32_t)sreg((int)sc_wave) + slot * SC_SLOT_B);
+    return rows;
+  };
+  auto issue_k81 = [&](int stage, int g) {
+    const int lt = g + s_lt0;
+    const unsigned char* kt = s_kb + (uint64_t)(uint32_t)lt * cs.kstep;
+    uint32_t koff8 = lane_k8;
+    if (!(lt > s_first && lt < s_last)) koff8 = (uint32_t)clamped(row8, rows_at(lt)) * cs.ks + kcol8;
+    dma16(kt, koff8, (uint32_t)sreg(lds0) + stage * TILE8_B + 1024 * wave);
+  };
+  // (SEG1) the walk's fixed addresses, from the cursor on the walk's first tile
+  auto seg1_enter = [&]() {
+    s_lt0 = cs.lt;
+    s_first = cs.la / BN;
+    s_last = cs.lt_end - 1;
+    s_kb = cs.kt - (int64_t)cs.lt * cs.kstep;
+    s_vb = cs.vt - (int64_t)cs.lt * cs.vstep;
+    if constexpr (FP8) {
+      s_ksc = cs.ksc - cs.lt;
+      s_vsc = cs.vsc - cs.lt;
+    }
+  };
   // this lane's 16 staged V codes of slot `slot` -> bf16 into V stage `stage` (row vrow8,
   // logical chunks 2 vj8 and 2 vj8 + 1); the tile's block scales -> sk, sv
   auto convert_v = [&](int slot, int stage, float& sk, float& sv) {
@@ -449,24 +489,23 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     i32x8 qh[2], ql[2];  // fp8: the query operands (hi, lo) of d-halves 0 and 1
     int sbh = 127, sbl = 127;  // and their e8m0 scales
     cursor_init<ESZ>(a, lo, hi, t0, b, h, cs);
+    if constexpr (SEG1) seg1_enter();
     if constexpr (FP8) {
       // tiles 0 and 1: staged V (slots 0, 1) and K (stages 0, 1)
       seg_offsets8();
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k)
         if (k < T) {
-          vr[k] = issue_raw(k);
-          issue_k8(k);
+          if constexpr (SEG1) {
+            vr[k] = issue_raw1(k, k);
+            issue_k81(k, k);
+          } else {
+            vr[k] = issue_raw(k);
+            issue_k8(k);
+          }
         }
     } else {
       seg_offsets();
-      if constexpr (SEG1) {
-        s_lt0 = cs.lt;
-        s_first = cs.la / BN;
-        s_last = cs.lt_end - 1;
-        s_kb = cs.kt - (int64_t)cs.lt * cs.kstep;
-        s_vb = cs.vt - (int64_t)cs.lt * cs.vstep;
-      }
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k)
         if (k < T) vr[k] = SEG1 ? issue1(k, k) : issue(k);
@@ -798,7 +837,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           wait_vm(1);
           convert_v((u + 1) & 1, SN, skr[1], svr[1]);
         }
-        if (u + 2 < T) vr[2] = issue_raw(u & 1);
+        if (u + 2 < T) vr[2] = SEG1 ? issue_raw1(u & 1, u + 2) : issue_raw(u & 1);
       }
       // step 2u reads the V fragments of step 2u+1 (tile u, already resident); step 2u+1 reads
       // those of step 2u+2 (tile u+1 rows 32..63, resident since the barrier, and tile u)
@@ -815,7 +854,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
       barrier_nofence();
       if constexpr (FP8) {
-        if (u + 2 < T) issue_k8(SP);
+        if (u + 2 < T) {
+          if constexpr (SEG1) issue_k81(SP, u + 2);
+          else issue_k8(SP);
+        }
       } else {
         if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = SEG1 ? issue1(SP, u + NSTAGE - 1) : issue(SP);
       }
@@ -981,7 +1023,9 @@ hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
 }
 
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {
-  return a.track_max ? launch<true, true>(a, stream) : launch<true, false>(a, stream);
+  if (a.track_max) return launch<true, true>(a, stream);
+  return a.nseg == 1 && a.mult_key < 0 ? launch<true, false, false, true>(a, stream)
+                                       : launch<true, false>(a, stream);
 }
 
 }  // namespace lbw
