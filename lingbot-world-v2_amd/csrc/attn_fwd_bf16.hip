@@ -180,10 +180,10 @@ __global__ void __launch_bounds__(64) attn_queue_reset_kernel(uint32_t* q) {
 // FOLD: scale * log2(e) == 1, i.e. q already carries log2(e)/sqrt(d) (a pre-scaled q, as the
 // fused q/k kernel writes it): the QK chain starts from -m instead of 0, so the MFMA result is
 // already the exponent of p and the softmax needs no per-score FMA (see the step).
-// SEG1: one KV segment and no multiplicity bias (a flat cache's window): the tile copies are
-// addressed by the tile index (issue1, issue_raw1, issue_k81) instead of walked by the general
-// cursor.
-template <bool FP8, bool TRACK, bool FOLD, bool SEG1>
+// SEGN = 1 or 2: that many KV segments (a flat cache's window; a cache and the current chunk),
+// no multiplicity bias and, for two, the same row strides: the tile copies are addressed by the
+// tile index (issue1, issue_raw1, issue_k81) instead of walked by the general cursor (SEGN 0).
+template <bool FP8, bool TRACK, bool FOLD, int SEGN>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   static_assert(!FOLD || (!FP8 && !TRACK), "the folded softmax is the plain bf16 form");
@@ -342,27 +342,34 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     if (cursor_next<ESZ>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets();
     return rows;
   };
-  // SEG1: tile g of the walk is local tile g + s_lt0 of the one segment; its K/V rows come from
-  // the index, and only the segment's first and last tiles compute their valid rows. Nothing is
-  // carried from one copy to the next, so the tile loop's only state is its counter.
-  int s_lt0 = 0, s_first = 0, s_last = 0;
-  const unsigned char* s_kb = nullptr;  // local tile 0 of the segment, (b, h)
-  const unsigned char* s_vb = nullptr;
-  const float* s_ksc = nullptr;         // fp8: the block scales of local tile 0
-  const float* s_vsc = nullptr;
-  // packed valid rows of local tile lt at the segment's ends (no bias)
-  auto rows_at = [&](int lt) -> int {
+  // SEGN > 0: walk tile g lies in the walk's first segment while g < w_g1, else in its second;
+  // it is local tile g + off of that segment, its K/V rows come from the index, and only a
+  // segment's first and last tiles compute their valid rows. Nothing is carried from one copy to
+  // the next, so the tile loop's only state is its counter.
+  struct SegWalk {
+    int off = 0, first = 0, last = 0, la = 0, lb = 0;  // local tile = g + off; ends; key range
+    const unsigned char* kb = nullptr;                  // local tile 0, (b, h)
+    const unsigned char* vb = nullptr;
+    const float* ksc = nullptr;                         // fp8: block scales of local tile 0
+    const float* vsc = nullptr;
+  };
+  SegWalk w0, w1;
+  int w_g1 = 1 << 30;
+  auto pick = [&](int g) -> SegWalk { return (SEGN == 2 && g >= w_g1) ? w1 : w0; };
+  // packed valid rows of local tile lt at a segment's ends (no bias)
+  auto rows_at = [&](const SegWalk& w, int lt) -> int {
     const int row0 = lt * BN;
-    const int l = cs.la - row0, u = cs.lb - row0;
+    const int l = w.la - row0, u = w.lb - row0;
     return pack_rows(l > 0 ? l : 0, u < BN ? u : BN, 255);
   };
   auto issue1 = [&](int stage, int g) -> int {
-    const int lt = g + s_lt0;
-    const unsigned char* kt = s_kb + (uint64_t)(uint32_t)lt * cs.kstep;
-    const unsigned char* vt = s_vb + (uint64_t)(uint32_t)lt * cs.vstep;
+    const SegWalk w = pick(g);
+    const int lt = g + w.off;
+    const unsigned char* kt = w.kb + (uint64_t)(uint32_t)lt * cs.kstep;
+    const unsigned char* vt = w.vb + (uint64_t)(uint32_t)lt * cs.vstep;
     const uint32_t kdst = (uint32_t)sreg((int)lds_wave) + stage * TILE_B;
     const uint32_t vdst = kdst + V_BASE;
-    if (lt > s_first && lt < s_last) {  // every row valid
+    if (lt > w.first && lt < w.last) {  // every row valid
 #pragma unroll
       for (int i = 0; i < NDMA; ++i) {
         dma16(kt, lane_k[i], kdst + 1024 * i);
@@ -370,7 +377,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
       return ROWS_FULL;
     }
-    const int rows = rows_at(lt);
+    const int rows = rows_at(w, lt);
     const int tvlo = rows & 0xff, rhi = ((rows >> 8) & 0xff) - 1;
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
@@ -426,38 +433,57 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     dma16(cs.kt, koff8, (uint32_t)sreg(lds0) + stage * TILE8_B + 1024 * wave);
     if (cursor_next<1>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets8();
   };
-  // SEG1 forms of the two: tile g of the walk, addressed by its index
+  // SEGN > 0 forms of the two: tile g of the walk, addressed by its index
   auto issue_raw1 = [&](int slot, int g) -> int {
-    const int lt = g + s_lt0;
-    const unsigned char* vt = s_vb + (uint64_t)(uint32_t)lt * cs.vstep;
+    const SegWalk w = pick(g);
+    const int lt = g + w.off;
+    const unsigned char* vt = w.vb + (uint64_t)(uint32_t)lt * cs.vstep;
     int rows = ROWS_FULL;
     uint32_t voff = lane_v8;
-    if (!(lt > s_first && lt < s_last)) {
-      rows = rows_at(lt);
+    if (!(lt > w.first && lt < w.last)) {
+      rows = rows_at(w, lt);
       voff = (uint32_t)clamped(vrow8, rows) * cs.vs + 16 * vj8;
     }
     dma16(vt, voff, (uint32_t)sreg((int)raw_wave) + slot * TILE8_B);
-    const uint64_t sp = (lane & 1) ? (uint64_t)(uintptr_t)(s_vsc + lt) : (uint64_t)(uintptr_t)(s_ksc + lt);
+    const uint64_t sp = (lane & 1) ? (uint64_t)(uintptr_t)(w.vsc + lt) : (uint64_t)(uintptr_t)(w.ksc + lt);
     dma4(sp, (uint32_t)sreg((int)sc_wave) + slot * SC_SLOT_B);
     return rows;
   };
   auto issue_k81 = [&](int stage, int g) {
-    const int lt = g + s_lt0;
-    const unsigned char* kt = s_kb + (uint64_t)(uint32_t)lt * cs.kstep;
+    const SegWalk w = pick(g);
+    const int lt = g + w.off;
+    const unsigned char* kt = w.kb + (uint64_t)(uint32_t)lt * cs.kstep;
     uint32_t koff8 = lane_k8;
-    if (!(lt > s_first && lt < s_last)) koff8 = (uint32_t)clamped(row8, rows_at(lt)) * cs.ks + kcol8;
+    if (!(lt > w.first && lt < w.last)) koff8 = (uint32_t)clamped(row8, rows_at(w, lt)) * cs.ks + kcol8;
     dma16(kt, koff8, (uint32_t)sreg(lds0) + stage * TILE8_B + 1024 * wave);
   };
-  // (SEG1) the walk's fixed addresses, from the cursor on the walk's first tile
-  auto seg1_enter = [&]() {
-    s_lt0 = cs.lt;
-    s_first = cs.la / BN;
-    s_last = cs.lt_end - 1;
-    s_kb = cs.kt - (int64_t)cs.lt * cs.kstep;
-    s_vb = cs.vt - (int64_t)cs.lt * cs.vstep;
+  // (SEGN > 0) the walk's fixed addresses: segment values from a cursor on walk tile g, the
+  // segment's first tile in the walk
+  auto walk_enter = [&](SegWalk& w, const TileCursor& c, int g) {
+    w.off = c.lt - g;
+    w.first = c.la / BN;
+    w.last = c.lt_end - 1;
+    w.la = c.la;
+    w.lb = c.lb;
+    w.kb = c.kt - (int64_t)c.lt * c.kstep;
+    w.vb = c.vt - (int64_t)c.lt * c.vstep;
     if constexpr (FP8) {
-      s_ksc = cs.ksc - cs.lt;
-      s_vsc = cs.vsc - cs.lt;
+      w.ksc = c.ksc - c.lt;
+      w.vsc = c.vsc - c.lt;
+    }
+  };
+  auto seg_walk_enter = [&]() {
+    walk_enter(w0, cs, 0);
+    if constexpr (SEGN == 2) {
+      // the next segment with keys, after the walk's tiles of the first
+      TileCursor c2 = cs;
+      const int n0 = cs.lt_end - cs.lt;
+      c2.lt = c2.lt_end - 1;
+      cursor_next<ESZ>(a, lo, hi, b, h, 0, c2);
+      if (c2.seg < a.nseg) {
+        w_g1 = n0;
+        walk_enter(w1, c2, n0);
+      }
     }
   };
   // this lane's 16 staged V codes of slot `slot` -> bf16 into V stage `stage` (row vrow8,
@@ -489,14 +515,14 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     i32x8 qh[2], ql[2];  // fp8: the query operands (hi, lo) of d-halves 0 and 1
     int sbh = 127, sbl = 127;  // and their e8m0 scales
     cursor_init<ESZ>(a, lo, hi, t0, b, h, cs);
-    if constexpr (SEG1) seg1_enter();
+    if constexpr (SEGN > 0) seg_walk_enter();
     if constexpr (FP8) {
       // tiles 0 and 1: staged V (slots 0, 1) and K (stages 0, 1)
       seg_offsets8();
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k)
         if (k < T) {
-          if constexpr (SEG1) {
+          if constexpr (SEGN > 0) {
             vr[k] = issue_raw1(k, k);
             issue_k81(k, k);
           } else {
@@ -508,7 +534,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       seg_offsets();
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k)
-        if (k < T) vr[k] = SEG1 ? issue1(k, k) : issue(k);
+        if (k < T) vr[k] = SEGN > 0 ? issue1(k, k) : issue(k);
     }
     // The first step's "previous sub-block" is the second half of stage NSTAGE-1's V tile
     // with P = 0: zero it so that 0 * V stays 0 (that stage is only filled after barrier 0).
@@ -837,7 +863,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           wait_vm(1);
           convert_v((u + 1) & 1, SN, skr[1], svr[1]);
         }
-        if (u + 2 < T) vr[2] = SEG1 ? issue_raw1(u & 1, u + 2) : issue_raw(u & 1);
+        if (u + 2 < T) vr[2] = SEGN > 0 ? issue_raw1(u & 1, u + 2) : issue_raw(u & 1);
       }
       // step 2u reads the V fragments of step 2u+1 (tile u, already resident); step 2u+1 reads
       // those of step 2u+2 (tile u+1 rows 32..63, resident since the barrier, and tile u)
@@ -855,11 +881,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       barrier_nofence();
       if constexpr (FP8) {
         if (u + 2 < T) {
-          if constexpr (SEG1) issue_k81(SP, u + 2);
+          if constexpr (SEGN > 0) issue_k81(SP, u + 2);
           else issue_k8(SP);
         }
       } else {
-        if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = SEG1 ? issue1(SP, u + NSTAGE - 1) : issue(SP);
+        if (u + NSTAGE - 1 < T) vr[NSTAGE - 1] = SEGN > 0 ? issue1(SP, u + NSTAGE - 1) : issue(SP);
       }
       if (wave_active)
         step(std::integral_constant<int, SN * KT_B>{},
@@ -993,9 +1019,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-template <bool FP8, bool TRACK, bool FOLD = false, bool SEG1 = false>
+template <bool FP8, bool TRACK, bool FOLD = false, int SEGN = 0>
 static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEG1>,
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t U = (uint32_t)a.n_qtiles * a.H * a.B;
@@ -1007,25 +1033,37 @@ static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
     nwg += 8u * ((per_xcd + 15u) / 16u);
     hipLaunchKernelGGL(attn_queue_reset_kernel, dim3(1), dim3(64), 0, stream, a.queue);
   }
-  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEG1>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
                      stream, a);
   return hipGetLastError();
 }
 
+// Segments the index-addressed copies take: 1, 2 (with equal row strides), or 0 for the cursor.
+static int index_segments(const AttnKernelArgs& a) {
+  if (a.mult_key >= 0) return 0;
+  if (a.nseg == 1) return 1;
+  if (a.nseg == 2 && a.seg[0].ksl == a.seg[1].ksl && a.seg[0].vsl == a.seg[1].vsl) return 2;
+  return 0;
+}
+
 hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
   if (a.track_max) return launch<false, true>(a, stream);
-  // a pre-scaled q (scale * log2(e) exactly 1 in fp32) takes the folded softmax; one segment
-  // with no multiplicity bias the index-addressed tile copies
-  const bool seg1 = a.nseg == 1 && a.mult_key < 0;
-  if (a.scale_log2 == 1.0f)
-    return seg1 ? launch<false, false, true, true>(a, stream) : launch<false, false, true>(a, stream);
-  return seg1 ? launch<false, false, false, true>(a, stream) : launch<false, false>(a, stream);
+  // a pre-scaled q (scale * log2(e) exactly 1 in fp32) takes the folded softmax
+  const int segn = index_segments(a);
+  if (a.scale_log2 == 1.0f) {
+    if (segn == 1) return launch<false, false, true, 1>(a, stream);
+    if (segn == 2) return launch<false, false, true, 2>(a, stream);
+    return launch<false, false, true>(a, stream);
+  }
+  if (segn == 1) return launch<false, false, false, 1>(a, stream);
+  if (segn == 2) return launch<false, false, false, 2>(a, stream);
+  return launch<false, false>(a, stream);
 }
 
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {
   if (a.track_max) return launch<true, true>(a, stream);
-  return a.nseg == 1 && a.mult_key < 0 ? launch<true, false, false, true>(a, stream)
-                                       : launch<true, false>(a, stream);
+  return index_segments(a) == 1 ? launch<true, false, false, 1>(a, stream)
+                                : launch<true, false>(a, stream);
 }
 
 }  // namespace lbw

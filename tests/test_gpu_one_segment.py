@@ -1,12 +1,15 @@
-"""The one-segment kernel instance (a call over one KV segment with no multiplicity bias: its
-tile copies are addressed by the tile index) against the general segment cursor and the oracle.
+"""The index-addressed kernel instances (a call over one KV segment, or two with the same row
+strides, and no multiplicity bias: their tile copies are addressed by the tile index) against the
+general segment cursor and the oracle.
 
-The same keys passed as two segments split at a multiple of 64 walk exactly the same 64-key tiles
-in the same order, so the general cursor must give the same output bit for bit; any error in the
-index addressing (a tile off by one, a wrong partial-tile row range at the window's ends, a piece
-of a split starting at the wrong tile) breaks that equality. The cases put the window's ends
-inside tiles, on tile boundaries and in one tile, split the keys into 1-5 pieces that start
-mid-segment, and limit keys per batch with k_lens; both softmax forms (plain and pre-scaled q)."""
+The same keys passed as one segment, as two segments split at a multiple of 64, and as three
+(the two and an empty one between them, which the index-addressed forms do not take) walk exactly
+the same 64-key tiles in the same order, so all three must give the same output bit for bit; any
+error in the index addressing (a tile off by one, a wrong partial-tile row range at the window's
+ends, a piece of a split starting at the wrong tile, the wrong segment for a tile) breaks that
+equality. The cases put the window's ends inside tiles, on tile boundaries and in one tile, split
+the keys into 1-5 pieces that start mid-segment, and limit keys per batch with k_lens; both
+softmax forms (plain and pre-scaled q)."""
 import math
 
 import pytest
@@ -34,7 +37,7 @@ CASES = [
 
 
 @pytest.mark.parametrize("i", range(len(CASES)))
-def test_one_segment_matches_general_cursor_and_oracle(lib, i):
+def test_index_addressed_match_general_cursor_and_oracle(lib, i):
     from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments, prescaled_q_scale
     B, H, Lq, L, win, splits, pre, klens, c = CASES[i]
     print(f"case {i}: B={B} H={H} Lq={Lq} L={L} window={win} splits={splits} pre={pre} "
@@ -55,10 +58,15 @@ def test_one_segment_matches_general_cursor_and_oracle(lib, i):
                              softmax_scale=scale)
     two = attention_segments(qd, [(kd[:, :c], vd[:, :c]), (kd[:, c:], vd[:, c:])], kv_lo=lo,
                              kv_hi=hi, k_lens=kl, num_splits=splits, softmax_scale=scale)
+    three = attention_segments(qd, [(kd[:, :c], vd[:, :c]), (kd[:, c:c], vd[:, c:c]),
+                                    (kd[:, c:], vd[:, c:])], kv_lo=lo, kv_hi=hi, k_lens=kl,
+                               num_splits=splits, softmax_scale=scale)
     torch.cuda.synchronize()
-    d = (one.float() - two.float()).abs()
-    print(f"  one vs two segments: max diff {float(d.max()):.3e}, differing {int((d > 0).sum())}")
-    assert torch.equal(one, two)
+    for name, x in (("one", one), ("two", two)):
+        d = (x.float() - three.float()).abs()
+        print(f"  {name} vs three segments: max diff {float(d.max()):.3e}, "
+              f"differing {int((d > 0).sum())}")
+    assert torch.equal(one, three) and torch.equal(two, three)
     kls = None if klens is None else torch.tensor(klens, dtype=torch.int32)
     ref = O.attention_ref(q, k, v, kv_lo=lo, kv_hi=hi, k_lens=kls,
                           softmax_scale=math.log(2.0) if pre else None)
