@@ -38,10 +38,11 @@ void check_bf16_4d(const char* name, const at::Tensor& t) {
   TORCH_CHECK(t.stride(3) == 1, name, " needs a contiguous head dim");
 }
 
-// Fills the params common to the attention ops (everything but the output).
+// Fills the params common to the attention ops (everything but the output); the K/V segments
+// hold kv_type elements (bf16, or the uint8 codes of the fp8 cache).
 lbw_attn_params base_params(const at::Tensor& q, at::TensorList k, at::TensorList v,
                             int64_t kv_lo, int64_t kv_hi, double softmax_scale,
-                            int64_t num_splits) {
+                            int64_t num_splits, at::ScalarType kv_type = at::kBFloat16) {
   check_bf16_4d("q", q);
   TORCH_CHECK(q.scalar_type() == at::kBFloat16, "q must be bf16");
   TORCH_CHECK(k.size() == v.size(), "k and v segment lists differ in length");
@@ -65,6 +66,8 @@ lbw_attn_params base_params(const at::Tensor& q, at::TensorList k, at::TensorLis
     check_bf16_4d("v", vt);
     TORCH_CHECK(kt.device() == q.device() && vt.device() == q.device(),
                 "k/v must be on q's device");
+    TORCH_CHECK(kt.scalar_type() == kv_type && vt.scalar_type() == kv_type, "k/v of segment ", i,
+                " must be ", kv_type == at::kByte ? "uint8 fp8 codes" : "bf16");
     TORCH_CHECK(kt.size(1) == vt.size(1), "k and v of segment ", i, " differ in length");
     lbw_kv_segment& s = p.seg[i];
     s.k = kt.data_ptr();
@@ -165,14 +168,17 @@ at::Tensor attention_fp8kv(const at::Tensor& q, at::TensorList k, at::TensorList
   c10::DeviceGuard guard(q.device());
   TORCH_CHECK(k_scale.size() == k.size() && v_scale.size() == k.size(),
               "one scale tensor per fp8 segment");
-  // the codes are uint8 [B, L, N, D]; base_params only reads their shapes and strides
-  lbw_attn_params p = base_params(q, k, v, kv_lo, kv_hi, softmax_scale, num_splits);
+  // the codes are uint8 [B, L, N, D]
+  lbw_attn_params p = base_params(q, k, v, kv_lo, kv_hi, softmax_scale, num_splits, at::kByte);
   for (size_t i = 0; i < k.size(); ++i) {
-    TORCH_CHECK(k[i].scalar_type() == at::kByte && v[i].scalar_type() == at::kByte,
-                "fp8 segments hold uint8 codes");
     TORCH_CHECK(k_scale[i].scalar_type() == at::kFloat && k_scale[i].is_contiguous() &&
-                    v_scale[i].scalar_type() == at::kFloat && v_scale[i].is_contiguous(),
-                "fp8 scales must be contiguous fp32 [B, N, nblk]");
+                    v_scale[i].scalar_type() == at::kFloat && v_scale[i].is_contiguous() &&
+                    k_scale[i].device() == q.device() && v_scale[i].device() == q.device(),
+                "fp8 scales must be contiguous fp32 [B, N, nblk] on q's device");
+    const int64_t nblk = (k[i].size(1) + LBW_FP8_BLOCK - 1) / LBW_FP8_BLOCK;
+    TORCH_CHECK(k_scale[i].numel() == k[i].size(0) * k[i].size(2) * nblk &&
+                    v_scale[i].numel() == k_scale[i].numel(),
+                "fp8 scales of segment ", i, " must be [B, N, ", nblk, "]");
     p.seg[i].k_scale = k_scale[i].data_ptr<float>();
     p.seg[i].v_scale = v_scale[i].data_ptr<float>();
   }
@@ -249,7 +255,52 @@ void qk_norm_rope_(const at::Tensor& q, const std::optional<at::Tensor>& k,
                    double q_scale, double k_scale, int64_t layout) {
   c10::DeviceGuard guard(q.device());
   TORCH_CHECK(rope_dims.size() == 5, "rope_dims = (f, h, w, s0, s1)");
-  TORCH_CHECK(q.dim() == 2 && q.scalar_type() == at::kBFloat16, "q must be bf16 [L, C] rows");
+  TORCH_CHECK(q.is_cuda() && q.dim() == 2 && q.scalar_type() == at::kBFloat16 && q.stride(1) == 1,
+              "q must be bf16 [L, C] rows on the GPU");
+  const int64_t C = q.size(1);
+  // every other tensor: bf16 on q's device (the RoPE tables fp32), the vectors of C elements
+  auto on_dev = [&](const at::Tensor& t, at::ScalarType st, const char* name) {
+    TORCH_CHECK(t.device() == q.device() && t.scalar_type() == st, name, " must be ",
+                st == at::kFloat ? "fp32" : "bf16", " on q's device");
+  };
+  auto vec = [&](const std::optional<at::Tensor>& t, const char* name) {
+    if (!t.has_value()) return;
+    on_dev(*t, at::kBFloat16, name);
+    TORCH_CHECK(t->is_contiguous() && t->numel() == C, name, " must be a contiguous [C] vector");
+  };
+  vec(bq, "bq");
+  vec(bk, "bk");
+  vec(wq, "wq");
+  vec(wk, "wk");
+  on_dev(rope, at::kFloat, "rope");
+  TORCH_CHECK(rope.is_contiguous(), "rope must be contiguous");
+  // [L, C] rows with a contiguous row; the outputs of the d-major layout are [H, D, L] with
+  // token stride 1 and head stride D * (d stride)
+  auto rows = [&](const at::Tensor& t, const char* name) {
+    on_dev(t, at::kBFloat16, name);
+    TORCH_CHECK(t.dim() == 2 && t.sizes() == q.sizes() && t.stride(1) == 1, name,
+                " must be [L, C] rows of q's shape");
+  };
+  auto out = [&](const at::Tensor& t, const char* name) {
+    if (layout != LBW_QK_DMAJOR) return rows(t, name);
+    on_dev(t, at::kBFloat16, name);
+    TORCH_CHECK(heads > 0 && C % heads == 0, "heads must divide C");
+    const int64_t D = C / heads;
+    TORCH_CHECK(t.dim() == 3 && t.size(0) == heads && t.size(1) == D && t.size(2) == q.size(0) &&
+                    t.stride(2) == 1 && t.stride(0) == D * t.stride(1),
+                name, " must be [H, D, L] with strides (D * s, s, 1)");
+  };
+  out(q_out, "q_out");
+  if (k.has_value()) {
+    rows(*k, "k");
+    TORCH_CHECK(k_out.has_value(), "k needs k_out");
+    out(*k_out, "k_out");
+  }
+  if (v.has_value()) {
+    rows(*v, "v");
+    TORCH_CHECK(v_out.has_value(), "v needs v_out");
+    rows(*v_out, "v_out");
+  }
   lbw_qk_norm_rope_params p;
   std::memset(&p, 0, sizeof(p));
   p.tokens = (int32_t)q.size(0);

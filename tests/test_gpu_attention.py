@@ -221,6 +221,43 @@ def test_errors_are_loud(lib):
         attention_segments(q, [(q, q)])
 
 
+def test_torch_ops_refuse_wrong_types_and_shapes(lib):
+    """The torch.ops.lbw operators, called directly (as a traced graph calls them, past the
+    Python wrappers' checks), refuse K/V, scales, weights and outputs of the wrong type, device
+    or shape with a RuntimeError before any kernel runs."""
+    from lbw_amd import _lib
+    _lib.ops()
+    ops = torch.ops.lbw
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16, device=DEV)
+    k32 = torch.zeros(1, 16, 2, 128, device=DEV)
+    with pytest.raises(RuntimeError, match="bf16"):
+        ops.attention(q, [k32], [k32], 0, -1, None, 0.0, 0, False)
+    kb = k32.to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="uint8"):
+        ops.attention_fp8kv(q, [kb], [kb], [torch.ones(1, 2, 1, device=DEV)],
+                            [torch.ones(1, 2, 1, device=DEV)], 0, -1, 0.0, 0, False)
+    codes = torch.zeros(1, 16, 2, 128, dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError, match="scales"):
+        ops.attention_fp8kv(q, [codes], [codes], [torch.ones(1, 2, 3, device=DEV)],
+                            [torch.ones(1, 2, 3, device=DEV)], 0, -1, 0.0, 0, False)
+    L, C = 8, 256
+    x = torch.zeros(L, C, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(C, dtype=torch.bfloat16, device=DEV)
+    rope = torch.zeros(1, device=DEV)
+    dims = [0, 0, 0, 22, 21]
+    with pytest.raises(RuntimeError, match="wq"):
+        ops.qk_norm_rope_(x, None, None, None, w.float(), None, rope, dims, 1e-6, 2, x.clone(),
+                          None, None, None, 1.0, 1.0, 0)
+    with pytest.raises(RuntimeError, match="v_out"):
+        ops.qk_norm_rope_(x, None, None, None, w, None, rope, dims, 1e-6, 2, x.clone(), None,
+                          x, x[:4], 1.0, 1.0, 0)
+    with pytest.raises(RuntimeError, match="q_out"):
+        ops.qk_norm_rope_(x, None, None, None, w, None, rope, dims, 1e-6, 2,
+                          torch.zeros(2, 128, L, dtype=torch.bfloat16, device=DEV)[:, :, :4],
+                          None, None, None, 1.0, 1.0, 1)
+    torch.cuda.synchronize()
+
+
 def test_two_streams_get_separate_workspaces(lib):
     """Two split-KV calls in flight on two streams at once: each call's workspace (work-queue
     counters and partials) comes from the caching allocator on its own stream, so neither call
