@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define LBW_ABI_VERSION 2
+#define LBW_ABI_VERSION 3
 #define LBW_MAX_KV_SEGMENTS 8
 #define LBW_FP8_BLOCK 64
 
@@ -87,6 +87,13 @@ typedef struct lbw_attn_params {
    * aligned, strides multiples of 4), the normalised O / l before any bf16 rounding: a check
    * of the kernels' own arithmetic apart from the output rounding (same kernels, same plan). */
   int32_t out_dtype;
+  /* Optional device int64 [1] window bounds, read by the kernel on the device, so that a caller
+   * whose window lives in device tensors (the flat cache's attn_lo / attn_hi,
+   * wan/modules/model_fast.py:2538-2550) needs no host synchronisation: the window is
+   * [max(kv_lo, *kv_lo_dev), min(kv_hi, *kv_hi_dev)) clamped to the keys. NULL = the host
+   * bounds alone. The split plan assumes the host window; cross-attention takes neither. */
+  const int64_t* kv_lo_dev;
+  const int64_t* kv_hi_dev;
 } lbw_attn_params;
 #define LBW_OUT_BF16 0
 #define LBW_OUT_FP32 1

@@ -32,6 +32,8 @@ struct AttnKernelArgs {
   SegDesc seg[LBW_MAX_SEGS];
   int64_t total;      // keys in the concatenation
   int64_t lo, hi;     // clamped window
+  const int64_t* lo_dev;  // device window bounds (narrow [lo, hi) on the device), or null
+  const int64_t* hi_dev;
   const int32_t* k_lens;
   float scale;        // softmax scale
   float scale_log2;   // scale * log2(e)

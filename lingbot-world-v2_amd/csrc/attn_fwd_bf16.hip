@@ -239,13 +239,22 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     // (waited for below, together with the first K/V tiles: one round trip, not two)
   }
 
-  // ---- key range of this batch and split
-  int64_t hi = a.hi;
+  // ---- key range of this batch and split (the host window, narrowed by the device bounds and
+  // k_lens when given)
+  int64_t hi = a.hi, lo = a.lo;
   if (a.k_lens != nullptr) {
     const int64_t kl = a.k_lens[b];
     hi = kl < hi ? kl : hi;
   }
-  const int64_t lo = a.lo;
+  if (a.hi_dev != nullptr) {
+    const int64_t x = *a.hi_dev;
+    hi = x < hi ? x : hi;
+  }
+  if (a.lo_dev != nullptr) {
+    const int64_t x = *a.lo_dev;
+    lo = x > lo ? x : lo;
+  }
+  if (hi < lo) hi = lo;
   const int n_tiles = hi > lo ? count_tiles(a, lo, hi) : 0;
   // this piece's tiles
   const int t0 = (int)((int64_t)n_tiles * split / a.splits);

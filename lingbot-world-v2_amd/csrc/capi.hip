@@ -200,6 +200,8 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   a.lo = p->kv_lo > 0 ? p->kv_lo : 0;
   a.hi = (p->kv_hi < 0 || p->kv_hi > start) ? start : p->kv_hi;
   if (a.hi < a.lo) a.hi = a.lo;
+  a.lo_dev = p->kv_lo_dev;
+  a.hi_dev = p->kv_hi_dev;
   a.k_lens = p->k_lens;
   const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf((float)p->head_dim);
   a.scale = scale;
@@ -369,6 +371,8 @@ int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream) {
   if (p->num_splits > 1) return fail(LBW_ERR_INVALID, "cross-attention is single pass");
   if (p->part_o != nullptr || p->part_m != nullptr || p->part_l != nullptr)
     return fail(LBW_ERR_INVALID, "cross-attention has no partials mode");
+  if (p->kv_lo_dev != nullptr || p->kv_hi_dev != nullptr)
+    return fail(LBW_ERR_INVALID, "cross-attention takes no device window bounds");
   lbw_attn_params q = *p;
   q.num_splits = 1;
   return run_attention(&q, false, nullptr, 0, stream, -1, 1.0, true);
@@ -383,7 +387,8 @@ int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, 
   if (n_distinct < 0 || n_distinct > L)
     return fail(LBW_ERR_INVALID, "n_distinct %lld not in [0, %lld]", (long long)n_distinct,
                 (long long)L);
-  if (p->k_lens != nullptr || p->kv_lo != 0 || p->kv_hi >= 0)
+  if (p->k_lens != nullptr || p->kv_lo != 0 || p->kv_hi >= 0 || p->kv_lo_dev != nullptr ||
+      p->kv_hi_dev != nullptr)
     return fail(LBW_ERR_INVALID, "dedup attends the whole context: no k_lens or window");
   if (p->num_splits > 1) return fail(LBW_ERR_INVALID, "cross-attention is single pass");
   if (p->part_o != nullptr || p->part_m != nullptr || p->part_l != nullptr)

@@ -38,6 +38,30 @@ void check_bf16_4d(const char* name, const at::Tensor& t) {
   TORCH_CHECK(t.stride(3) == 1, name, " needs a contiguous head dim");
 }
 
+// A device window bound: a one-element integer tensor on q's device (the flat cache's attn_lo /
+// attn_hi, model_fast.py:2538-2550). The kernel reads it on the device; a bound of another
+// integer type is converted to int64 there (queued on the current stream, no host sync), and
+// `keep` holds the converted tensor until the call has been queued.
+const int64_t* dev_bound(const std::optional<at::Tensor>& t, const at::Tensor& q, at::Tensor& keep,
+                         const char* name) {
+  if (!t.has_value()) return nullptr;
+  TORCH_CHECK(t->device() == q.device() && t->numel() == 1 &&
+                  at::isIntegralType(t->scalar_type(), /*includeBool=*/false),
+              name, " must be a one-element integer tensor on q's device");
+  keep = t->scalar_type() == at::kLong ? *t : t->to(at::kLong);
+  return keep.data_ptr<int64_t>();
+}
+
+// The device bounds of a call, converted where needed (see dev_bound).
+struct DevBounds {
+  at::Tensor lo, hi;
+  void set(lbw_attn_params& p, const std::optional<at::Tensor>& kv_lo_dev,
+           const std::optional<at::Tensor>& kv_hi_dev, const at::Tensor& q) {
+    p.kv_lo_dev = dev_bound(kv_lo_dev, q, lo, "kv_lo_dev");
+    p.kv_hi_dev = dev_bound(kv_hi_dev, q, hi, "kv_hi_dev");
+  }
+};
+
 // Fills the params common to the attention ops (everything but the output); the K/V segments
 // hold kv_type elements (bf16, or the uint8 codes of the fp8 cache).
 lbw_attn_params base_params(const at::Tensor& q, at::TensorList k, at::TensorList v,
@@ -124,31 +148,37 @@ void run_with_workspace(const lbw_attn_params& p, const at::Tensor& q, Fn fn, Si
 
 void attention_out(const at::Tensor& q, at::TensorList k, at::TensorList v, int64_t kv_lo,
                    int64_t kv_hi, const std::optional<at::Tensor>& k_lens, double softmax_scale,
-                   int64_t num_splits, const at::Tensor& out) {
+                   int64_t num_splits, const at::Tensor& out,
+                   const std::optional<at::Tensor>& kv_lo_dev,
+                   const std::optional<at::Tensor>& kv_hi_dev) {
   c10::DeviceGuard guard(q.device());
   lbw_attn_params p = base_params(q, k, v, kv_lo, kv_hi, softmax_scale, num_splits);
   set_out(p, out, q);
   set_k_lens(p, k_lens, q);
+  DevBounds db;
+  db.set(p, kv_lo_dev, kv_hi_dev, q);
   run_with_workspace(p, q, lbw_attention_fwd, lbw_attention_workspace_size, "lbw_attention_fwd");
 }
 
 at::Tensor attention(const at::Tensor& q, at::TensorList k, at::TensorList v, int64_t kv_lo,
                      int64_t kv_hi, const std::optional<at::Tensor>& k_lens, double softmax_scale,
-                     int64_t num_splits, bool out_fp32) {
+                     int64_t num_splits, bool out_fp32, const std::optional<at::Tensor>& kv_lo_dev,
+                     const std::optional<at::Tensor>& kv_hi_dev) {
   at::Tensor out = new_out(q, out_fp32);
-  attention_out(q, k, v, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, out);
+  attention_out(q, k, v, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, out, kv_lo_dev,
+                kv_hi_dev);
   return out;
 }
 
-at::Tensor cross_attention(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
-                           const std::optional<at::Tensor>& k_lens, int64_t n_distinct,
-                           int64_t kv_lo, int64_t kv_hi, double softmax_scale, bool out_fp32) {
+void cross_attention_out(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                         const std::optional<at::Tensor>& k_lens, int64_t n_distinct,
+                         int64_t kv_lo, int64_t kv_hi, double softmax_scale,
+                         const at::Tensor& out) {
   c10::DeviceGuard guard(q.device());
   const at::Tensor ks[1] = {k};
   const at::Tensor vs[1] = {v};
   lbw_attn_params p = base_params(q, at::TensorList(ks, 1), at::TensorList(vs, 1), kv_lo, kv_hi,
                                   softmax_scale, 1);
-  at::Tensor out = new_out(q, out_fp32);
   set_out(p, out, q);
   set_k_lens(p, k_lens, q);
   if (n_distinct >= 0) {
@@ -158,13 +188,21 @@ at::Tensor cross_attention(const at::Tensor& q, const at::Tensor& k, const at::T
   } else {
     check(lbw_cross_attention_fwd(&p, stream_of(q)), "lbw_cross_attention_fwd");
   }
+}
+
+at::Tensor cross_attention(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                           const std::optional<at::Tensor>& k_lens, int64_t n_distinct,
+                           int64_t kv_lo, int64_t kv_hi, double softmax_scale, bool out_fp32) {
+  at::Tensor out = new_out(q, out_fp32);
+  cross_attention_out(q, k, v, k_lens, n_distinct, kv_lo, kv_hi, softmax_scale, out);
   return out;
 }
 
-at::Tensor attention_fp8kv(const at::Tensor& q, at::TensorList k, at::TensorList v,
-                           at::TensorList k_scale, at::TensorList v_scale, int64_t kv_lo,
-                           int64_t kv_hi, double softmax_scale, int64_t num_splits,
-                           bool out_fp32) {
+void attention_fp8kv_out(const at::Tensor& q, at::TensorList k, at::TensorList v,
+                         at::TensorList k_scale, at::TensorList v_scale, int64_t kv_lo,
+                         int64_t kv_hi, double softmax_scale, int64_t num_splits,
+                         const at::Tensor& out, const std::optional<at::Tensor>& kv_lo_dev,
+                         const std::optional<at::Tensor>& kv_hi_dev) {
   c10::DeviceGuard guard(q.device());
   TORCH_CHECK(k_scale.size() == k.size() && v_scale.size() == k.size(),
               "one scale tensor per fp8 segment");
@@ -182,18 +220,32 @@ at::Tensor attention_fp8kv(const at::Tensor& q, at::TensorList k, at::TensorList
     p.seg[i].k_scale = k_scale[i].data_ptr<float>();
     p.seg[i].v_scale = v_scale[i].data_ptr<float>();
   }
-  at::Tensor out = new_out(q, out_fp32);
   set_out(p, out, q);
+  DevBounds db;
+  db.set(p, kv_lo_dev, kv_hi_dev, q);
   run_with_workspace(p, q, lbw_attention_fwd_fp8kv, lbw_attention_fp8kv_workspace_size,
                      "lbw_attention_fwd_fp8kv");
+}
+
+at::Tensor attention_fp8kv(const at::Tensor& q, at::TensorList k, at::TensorList v,
+                           at::TensorList k_scale, at::TensorList v_scale, int64_t kv_lo,
+                           int64_t kv_hi, double softmax_scale, int64_t num_splits,
+                           bool out_fp32, const std::optional<at::Tensor>& kv_lo_dev,
+                           const std::optional<at::Tensor>& kv_hi_dev) {
+  at::Tensor out = new_out(q, out_fp32);
+  attention_fp8kv_out(q, k, v, k_scale, v_scale, kv_lo, kv_hi, softmax_scale, num_splits, out,
+                      kv_lo_dev, kv_hi_dev);
   return out;
 }
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor> attention_partial(
     const at::Tensor& q, at::TensorList k, at::TensorList v, int64_t kv_lo, int64_t kv_hi,
-    double softmax_scale) {
+    double softmax_scale, const std::optional<at::Tensor>& kv_lo_dev,
+    const std::optional<at::Tensor>& kv_hi_dev) {
   c10::DeviceGuard guard(q.device());
   lbw_attn_params p = base_params(q, k, v, kv_lo, kv_hi, softmax_scale, 1);
+  DevBounds db;
+  db.set(p, kv_lo_dev, kv_hi_dev, q);
   const int64_t B = q.size(0), Lq = q.size(1), H = q.size(2), D = q.size(3);
   at::Tensor po = at::empty({B, H, Lq, D}, q.options().dtype(at::kFloat));
   at::Tensor pm = at::empty({B, H, Lq}, q.options().dtype(at::kFloat));
@@ -209,13 +261,17 @@ void attention_merge_out(at::TensorList o, at::TensorList m, at::TensorList l,
                          const at::Tensor& out) {
   TORCH_CHECK(o.size() >= 1 && o.size() <= 16 && m.size() == o.size() && l.size() == o.size(),
               "1..16 partials of (O, m, l)");
-  c10::DeviceGuard guard(o[0].device());
+  TORCH_CHECK(out.is_cuda() && o[0].dim() == 4, "out must be a GPU tensor, O [B, N, Lq, D]");
+  c10::DeviceGuard guard(out.device());
   const int64_t B = o[0].size(0), H = o[0].size(1), Lq = o[0].size(2), D = o[0].size(3);
   std::vector<const float*> po, pm, pl;
   for (size_t i = 0; i < o.size(); ++i) {
-    TORCH_CHECK(o[i].sizes() == o[0].sizes() && m[i].dim() == 3 && m[i].size(2) == Lq &&
-                    l[i].sizes() == m[i].sizes(),
-                "partials differ in shape");
+    TORCH_CHECK(o[i].sizes() == o[0].sizes() && m[i].dim() == 3 && m[i].size(0) == B &&
+                    m[i].size(1) == H && m[i].size(2) == Lq && l[i].sizes() == m[i].sizes(),
+                "partials differ in shape: O [B, N, Lq, D], m and l [B, N, Lq]");
+    TORCH_CHECK(o[i].device() == out.device() && m[i].device() == out.device() &&
+                    l[i].device() == out.device(),
+                "partials must be on out's device");
     TORCH_CHECK(o[i].is_contiguous() && m[i].is_contiguous() && l[i].is_contiguous() &&
                     o[i].scalar_type() == at::kFloat && m[i].scalar_type() == at::kFloat &&
                     l[i].scalar_type() == at::kFloat,
@@ -274,6 +330,11 @@ void qk_norm_rope_(const at::Tensor& q, const std::optional<at::Tensor>& k,
   vec(wk, "wk");
   on_dev(rope, at::kFloat, "rope");
   TORCH_CHECK(rope.is_contiguous(), "rope must be contiguous");
+  // the packed per-axis tables: cos and sin of f x s0, h x s1 and w x s1 angles
+  const int64_t ntab = 2 * (rope_dims[0] * rope_dims[3] + (rope_dims[1] + rope_dims[2]) * rope_dims[4]);
+  TORCH_CHECK(rope_dims[0] >= 0 && rope_dims[1] >= 0 && rope_dims[2] >= 0 && rope_dims[3] >= 0 &&
+                  rope_dims[4] >= 0 && rope.numel() >= ntab,
+              "rope holds ", rope.numel(), " floats; rope_dims ", rope_dims, " need ", ntab);
   // [L, C] rows with a contiguous row; the outputs of the d-major layout are [H, D, L] with
   // token stride 1 and head stride D * (d stride)
   auto rows = [&](const at::Tensor& t, const char* name) {
@@ -350,6 +411,11 @@ void kv_quant_fp8_(const at::Tensor& x, const at::Tensor& codes, const at::Tenso
               "codes must be contiguous uint8 of x's shape");
   TORCH_CHECK(scales.scalar_type() == at::kFloat && scales.is_contiguous(),
               "scales must be contiguous fp32");
+  TORCH_CHECK(codes.device() == x.device() && scales.device() == x.device(),
+              "codes and scales must be on x's device");
+  const int64_t nblk = (x.size(1) + LBW_FP8_BLOCK - 1) / LBW_FP8_BLOCK;
+  TORCH_CHECK(scales.numel() == x.size(0) * x.size(2) * nblk, "scales must be [B, N, ", nblk,
+              "] (", x.size(0) * x.size(2) * nblk, " floats), got ", scales.numel());
   check(lbw_kv_quant_fp8(x.data_ptr(), (int32_t)x.size(0), x.size(1), (int32_t)x.size(2),
                          (int32_t)x.size(3), x.stride(0), x.stride(1), x.stride(2),
                          codes.data_ptr<uint8_t>(), scales.data_ptr<float>(), LBW_FP8_BLOCK,
@@ -358,8 +424,9 @@ void kv_quant_fp8_(const at::Tensor& x, const at::Tensor& codes, const at::Tenso
 }
 
 // ---- shapes for tracing (Meta / fake tensors): outputs only, no work
+using OptT = std::optional<at::Tensor>;
 at::Tensor attention_meta(const at::Tensor& q, at::TensorList, at::TensorList, int64_t, int64_t,
-                          const std::optional<at::Tensor>&, double, int64_t, bool out_fp32) {
+                          const OptT&, double, int64_t, bool out_fp32, const OptT&, const OptT&) {
   return new_out(q, out_fp32);
 }
 at::Tensor cross_attention_meta(const at::Tensor& q, const at::Tensor&, const at::Tensor&,
@@ -369,11 +436,17 @@ at::Tensor cross_attention_meta(const at::Tensor& q, const at::Tensor&, const at
 }
 at::Tensor attention_fp8kv_meta(const at::Tensor& q, at::TensorList, at::TensorList,
                                 at::TensorList, at::TensorList, int64_t, int64_t, double,
-                                int64_t, bool out_fp32) {
+                                int64_t, bool out_fp32, const OptT&, const OptT&) {
   return new_out(q, out_fp32);
 }
+void attention_fp8kv_out_meta(const at::Tensor&, at::TensorList, at::TensorList, at::TensorList,
+                              at::TensorList, int64_t, int64_t, double, int64_t,
+                              const at::Tensor&, const OptT&, const OptT&) {}
+void cross_attention_out_meta(const at::Tensor&, const at::Tensor&, const at::Tensor&,
+                              const OptT&, int64_t, int64_t, int64_t, double, const at::Tensor&) {}
 std::tuple<at::Tensor, at::Tensor, at::Tensor> attention_partial_meta(
-    const at::Tensor& q, at::TensorList, at::TensorList, int64_t, int64_t, double) {
+    const at::Tensor& q, at::TensorList, at::TensorList, int64_t, int64_t, double, const OptT&,
+    const OptT&) {
   const int64_t B = q.size(0), Lq = q.size(1), H = q.size(2), D = q.size(3);
   auto f = q.options().dtype(at::kFloat);
   return {at::empty({B, H, Lq, D}, f), at::empty({B, H, Lq}, f), at::empty({B, H, Lq}, f)};
@@ -383,7 +456,8 @@ at::Tensor attention_merge_meta(at::TensorList o, at::TensorList, at::TensorList
                    o[0].options().dtype(at::kBFloat16));
 }
 void attention_out_meta(const at::Tensor&, at::TensorList, at::TensorList, int64_t, int64_t,
-                        const std::optional<at::Tensor>&, double, int64_t, const at::Tensor&) {}
+                        const OptT&, double, int64_t, const at::Tensor&, const OptT&,
+                        const OptT&) {}
 void attention_merge_out_meta(at::TensorList, at::TensorList, at::TensorList,
                               const at::Tensor&) {}
 void qk_norm_rope_meta(const at::Tensor&, const std::optional<at::Tensor>&,
@@ -397,18 +471,27 @@ void kv_quant_fp8_meta(const at::Tensor&, const at::Tensor&, const at::Tensor&) 
 }  // namespace
 
 TORCH_LIBRARY(lbw, m) {
+  // kv_lo_dev / kv_hi_dev: one-element integer tensors on q's device (the window read on the
+  // device, no host sync); they narrow the host window kv_lo / kv_hi
   m.def("attention(Tensor q, Tensor[] k, Tensor[] v, int kv_lo=0, int kv_hi=-1, "
-        "Tensor? k_lens=None, float softmax_scale=0., int num_splits=0, bool out_fp32=False) "
-        "-> Tensor");
+        "Tensor? k_lens=None, float softmax_scale=0., int num_splits=0, bool out_fp32=False, "
+        "Tensor? kv_lo_dev=None, Tensor? kv_hi_dev=None) -> Tensor");
   m.def("attention_out(Tensor q, Tensor[] k, Tensor[] v, int kv_lo, int kv_hi, Tensor? k_lens, "
-        "float softmax_scale, int num_splits, Tensor(a!) out) -> ()");
+        "float softmax_scale, int num_splits, Tensor(a!) out, Tensor? kv_lo_dev=None, "
+        "Tensor? kv_hi_dev=None) -> ()");
   m.def("cross_attention(Tensor q, Tensor k, Tensor v, Tensor? k_lens=None, int n_distinct=-1, "
         "int kv_lo=0, int kv_hi=-1, float softmax_scale=0., bool out_fp32=False) -> Tensor");
+  m.def("cross_attention_out(Tensor q, Tensor k, Tensor v, Tensor? k_lens, int n_distinct, "
+        "int kv_lo, int kv_hi, float softmax_scale, Tensor(a!) out) -> ()");
   m.def("attention_fp8kv(Tensor q, Tensor[] k, Tensor[] v, Tensor[] k_scale, Tensor[] v_scale, "
         "int kv_lo=0, int kv_hi=-1, float softmax_scale=0., int num_splits=0, "
-        "bool out_fp32=False) -> Tensor");
+        "bool out_fp32=False, Tensor? kv_lo_dev=None, Tensor? kv_hi_dev=None) -> Tensor");
+  m.def("attention_fp8kv_out(Tensor q, Tensor[] k, Tensor[] v, Tensor[] k_scale, "
+        "Tensor[] v_scale, int kv_lo, int kv_hi, float softmax_scale, int num_splits, "
+        "Tensor(a!) out, Tensor? kv_lo_dev=None, Tensor? kv_hi_dev=None) -> ()");
   m.def("attention_partial(Tensor q, Tensor[] k, Tensor[] v, int kv_lo=0, int kv_hi=-1, "
-        "float softmax_scale=0.) -> (Tensor, Tensor, Tensor)");
+        "float softmax_scale=0., Tensor? kv_lo_dev=None, Tensor? kv_hi_dev=None) "
+        "-> (Tensor, Tensor, Tensor)");
   m.def("attention_merge(Tensor[] o, Tensor[] m, Tensor[] l) -> Tensor");
   m.def("attention_merge_out(Tensor[] o, Tensor[] m, Tensor[] l, Tensor(a!) out) -> ()");
   m.def("qk_norm_rope_(Tensor q, Tensor? k, Tensor? bq, Tensor? bk, Tensor wq, Tensor? wk, "
@@ -422,7 +505,9 @@ TORCH_LIBRARY_IMPL(lbw, CUDA, m) {
   m.impl("attention", &attention);
   m.impl("attention_out", &attention_out);
   m.impl("cross_attention", &cross_attention);
+  m.impl("cross_attention_out", &cross_attention_out);
   m.impl("attention_fp8kv", &attention_fp8kv);
+  m.impl("attention_fp8kv_out", &attention_fp8kv_out);
   m.impl("attention_partial", &attention_partial);
   m.impl("attention_merge", &attention_merge);
   m.impl("attention_merge_out", &attention_merge_out);
@@ -434,7 +519,9 @@ TORCH_LIBRARY_IMPL(lbw, Meta, m) {
   m.impl("attention", &attention_meta);
   m.impl("attention_out", &attention_out_meta);
   m.impl("cross_attention", &cross_attention_meta);
+  m.impl("cross_attention_out", &cross_attention_out_meta);
   m.impl("attention_fp8kv", &attention_fp8kv_meta);
+  m.impl("attention_fp8kv_out", &attention_fp8kv_out_meta);
   m.impl("attention_partial", &attention_partial_meta);
   m.impl("attention_merge", &attention_merge_meta);
   m.impl("attention_merge_out", &attention_merge_out_meta);

@@ -17,7 +17,7 @@ OPS_PATH = os.path.join(_HERE, "liblbw_torch.so")
 
 MAX_KV_SEGMENTS = 8
 FP8_BLOCK = 64
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OUT_BF16 = 0
 OUT_FP32 = 1
@@ -51,6 +51,7 @@ class AttnParams(ctypes.Structure):
         ("num_splits", ctypes.c_int32),
         ("part_o", ctypes.c_void_p), ("part_m", ctypes.c_void_p), ("part_l", ctypes.c_void_p),
         ("out_dtype", ctypes.c_int32),
+        ("kv_lo_dev", ctypes.c_void_p), ("kv_hi_dev", ctypes.c_void_p),
     ]
 
 
@@ -166,7 +167,8 @@ def attn_params(q, out, segments, kv_lo=None, kv_hi=None, k_lens=None, softmax_s
                 num_splits=0, parts=None) -> AttnParams:
     """``lbw_attn_params`` for direct calls of the C ABI: q ``[B, Lq, N, D]``, out of q's shape
     (bf16 or fp32) or None, segments ``[(k, v)]`` or ``[(k, v, k_scale, v_scale)]`` (fp8),
-    optional partial outputs ``(O, m, l)``."""
+    optional partial outputs ``(O, m, l)``. ``kv_lo`` / ``kv_hi`` may be one-element int64
+    tensors on q's device (read by the kernel on the device)."""
     import torch
     p = AttnParams()
     B, Lq, H, D = q.shape
@@ -188,8 +190,16 @@ def attn_params(q, out, segments, kv_lo=None, kv_hi=None, k_lens=None, softmax_s
         seg.v_stride_b, seg.v_stride_l, seg.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
         if len(sg) > 2:
             seg.k_scale, seg.v_scale = sg[2].data_ptr(), sg[3].data_ptr()
-    p.kv_lo = 0 if kv_lo is None else int(kv_lo)
-    p.kv_hi = -1 if kv_hi is None else int(kv_hi)
+    p.kv_lo, p.kv_hi = 0, -1
+    for name, b in (("lo", kv_lo), ("hi", kv_hi)):
+        if b is None:
+            continue
+        if torch.is_tensor(b) and b.device.type != "cpu":
+            if b.dtype != torch.int64 or b.numel() != 1:
+                raise ValueError(f"kv_{name} on the device must be a one-element int64 tensor")
+            setattr(p, f"kv_{name}_dev", b.data_ptr())
+        else:
+            setattr(p, f"kv_{name}", int(b))
     p.k_lens = k_lens.data_ptr() if k_lens is not None else None
     p.softmax_scale = 0.0 if softmax_scale is None else float(softmax_scale)
     p.num_splits = int(num_splits)

@@ -52,6 +52,24 @@ def _check_4d(name, t, device):
         raise RuntimeError(f"{name} must be a GPU tensor (the path has no CPU implementation)")
 
 
+def _bounds(kv_lo, kv_hi, device):
+    """(host lo, host hi, device lo, device hi) of a window given as ints, host tensors or
+    one-element integer tensors on ``device`` (read there by the kernel: no host sync)."""
+    out = []
+    for b, default in ((kv_lo, 0), (kv_hi, -1)):
+        if b is None:
+            out.append((default, None))
+        elif torch.is_tensor(b) and b.device.type != "cpu":
+            if b.device != device or b.numel() != 1 or b.dtype.is_floating_point or b.dtype == torch.bool:
+                raise ValueError("a device window bound must be a one-element integer tensor "
+                                 "on q's device")
+            out.append((default, b.reshape(1)))
+        else:
+            out.append((int(b), None))
+    (lo, dlo), (hi, dhi) = out
+    return lo, hi, dlo, dhi
+
+
 def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi=None,
                        k_lens: torch.Tensor | None = None, softmax_scale=None,
                        num_splits: int = 0, out: torch.Tensor | None = None,
@@ -61,7 +79,8 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
 
     q ``[B, Lq, N, 128]``; each segment is ``(k, v)`` with k/v ``[B, L_i, N, 128]`` (strided
     views are fine as long as the head dim is contiguous); the window ``[kv_lo, kv_hi)``
-    indexes the concatenation. ``k_lens`` (int32 ``[B]`` on the device) limits each batch's
+    indexes the concatenation (ints, or one-element integer tensors on q's device that the
+    kernel reads there, so the call needs no host sync). ``k_lens`` (int32 ``[B]`` on the device) limits each batch's
     keys. With ``cross``, a single short segment; ``n_distinct`` (cross only) declares keys
     ``n_distinct..`` identical rows, attended as one key of that multiplicity (exact).
     Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given). ``out_dtype=torch.float32``
@@ -73,8 +92,7 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     q = _as_bf16(q)
     ks, vs = _segments(segments, device)
     scale = 0.0 if softmax_scale is None else float(softmax_scale)
-    lo = 0 if kv_lo is None else int(kv_lo)
-    hi = -1 if kv_hi is None else int(kv_hi)
+    lo, hi, dlo, dhi = _bounds(kv_lo, kv_hi, device)
     if out is not None:
         if out.dtype not in (torch.bfloat16, torch.float32) or out.shape != q.shape:
             raise ValueError("out must be a bf16 or fp32 tensor of q's shape")
@@ -85,15 +103,18 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     if cross:
         if len(ks) != 1:
             raise ValueError("cross-attention takes one KV segment")
-        fp32 = (out.dtype if out is not None else out_dtype) == torch.float32
-        res = ops.cross_attention(q, ks[0], vs[0], k_lens,
-                                  -1 if n_distinct is None else int(n_distinct), lo, hi, scale,
-                                  fp32)
-        return res if out is None else out.copy_(res)
+        if dlo is not None or dhi is not None:
+            raise ValueError("cross-attention takes no device window bounds")
+        nd = -1 if n_distinct is None else int(n_distinct)
+        if out is None:
+            return ops.cross_attention(q, ks[0], vs[0], k_lens, nd, lo, hi, scale,
+                                       out_dtype == torch.float32)
+        ops.cross_attention_out(q, ks[0], vs[0], k_lens, nd, lo, hi, scale, out)
+        return out
     if out is None:
         return ops.attention(q, ks, vs, lo, hi, k_lens, scale, int(num_splits),
-                             out_dtype == torch.float32)
-    ops.attention_out(q, ks, vs, lo, hi, k_lens, scale, int(num_splits), out)
+                             out_dtype == torch.float32, dlo, dhi)
+    ops.attention_out(q, ks, vs, lo, hi, k_lens, scale, int(num_splits), out, dlo, dhi)
     return out
 
 
@@ -127,10 +148,6 @@ def window_from_mask(attn_mask: torch.Tensor, lk: int):
     return lo, hi
 
 
-def _scalar(x):
-    return int(x.item()) if torch.is_tensor(x) else int(x)
-
-
 def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=None,
               q_scale=None, causal=False, window_size=(-1, -1), deterministic=False,
               dtype=torch.bfloat16, fa_version=None, attn_mask=None, is_cross_attn=False,
@@ -138,12 +155,15 @@ def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=Non
     """attention.py:1082-1143 with the reference's signature and layout.
 
     Differences from the reference's SDPA fallback, all loud: ``causal=True``,
-    ``dropout_p > 0`` and masks that are not a KV window raise. ``kv_lo``/``kv_hi`` (ints
-    or 0-d tensors) take precedence over ``attn_mask`` (they carry the same window,
-    model_fast.py:2546-2550). ``q_lens``/``k_lens`` are ignored with the reference's
-    warning (attention.py:1128-1132); masked cross-attention is ``cross_attention``.
-    The kernels compute in bf16, so ``dtype`` must be ``torch.bfloat16`` (the reference
-    computes in ``dtype``; any other value raises). Output: bf16 ``[B, Lq, N, D]``."""
+    ``dropout_p > 0`` and masks that are not a KV window raise. ``kv_lo``/``kv_hi`` take
+    precedence over ``attn_mask`` (they carry the same window, model_fast.py:2546-2550); as
+    the reference passes them -- one-element tensors on the device (``attn_lo``,
+    ``attn_hi``) -- the kernel reads them there and the call never synchronises the host.
+    ``q_lens``/``k_lens`` are ignored with the reference's warning (attention.py:1128-1132);
+    masked cross-attention is ``cross_attention``. ``q_scale`` is ignored, as the reference
+    ignores it on every path (attention.py:1082-1143), with a warning. The kernels compute in
+    bf16, so ``dtype`` must be ``torch.bfloat16`` (the reference computes in ``dtype``; any
+    other value raises). Output: bf16 ``[B, Lq, N, D]``."""
     _check_dtype(dtype)
     if causal:
         raise NotImplementedError("causal masking is not part of this path (the chunked "
@@ -156,13 +176,14 @@ def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=Non
         warnings.warn('Padding mask is disabled when using scaled_dot_product_attention. '
                       'It can have a significant impact on performance.')
     if q_scale is not None:
-        q = q * q_scale
-    lo = _scalar(kv_lo) if kv_lo is not None else None
-    hi = _scalar(kv_hi) if kv_hi is not None else None
+        warnings.warn("q_scale is ignored, as in the reference's attention() "
+                      "(wan/modules/attention.py:1082-1143)")
+    lo, hi = kv_lo, kv_hi
     if attn_mask is not None and lo is None and hi is None:
         lo, hi = window_from_mask(attn_mask, k.shape[1])
+    on_dev = any(torch.is_tensor(b) and b.device.type != "cpu" for b in (lo, hi))
     out = attention_segments(q, [(k, v)], kv_lo=lo, kv_hi=hi, softmax_scale=softmax_scale,
-                             cross=bool(is_cross_attn) and k.shape[1] <= 4096)
+                             cross=bool(is_cross_attn) and k.shape[1] <= 4096 and not on_dev)
     return out
 
 
@@ -225,9 +246,9 @@ def attention_partial(q, segments, *, kv_lo=None, kv_hi=None, softmax_scale=None
     _check_4d("q", q, device)
     q = _as_bf16(q)
     ks, vs = _segments(segments, device)
-    return ops.attention_partial(q, ks, vs, 0 if kv_lo is None else int(kv_lo),
-                                 -1 if kv_hi is None else int(kv_hi),
-                                 0.0 if softmax_scale is None else float(softmax_scale))
+    lo, hi, dlo, dhi = _bounds(kv_lo, kv_hi, device)
+    return ops.attention_partial(q, ks, vs, lo, hi,
+                                 0.0 if softmax_scale is None else float(softmax_scale), dlo, dhi)
 
 
 def attention_merge(parts, out: torch.Tensor | None = None) -> torch.Tensor:

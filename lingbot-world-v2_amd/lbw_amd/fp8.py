@@ -13,7 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .attention import _as_bf16, _check_4d
+from .attention import _as_bf16, _bounds, _check_4d
 
 __all__ = ["Fp8KV", "quantize_kv_fp8", "attention_fp8kv"]
 
@@ -71,9 +71,12 @@ def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softma
         vc.append(v.codes)
         ksc.append(k.scales)
         vsc.append(v.scales)
-    lo = 0 if kv_lo is None else int(kv_lo)
-    hi = -1 if kv_hi is None else int(kv_hi)
+    lo, hi, dlo, dhi = _bounds(kv_lo, kv_hi, device)
     scale = 0.0 if softmax_scale is None else float(softmax_scale)
-    res = ops.attention_fp8kv(q, kc, vc, ksc, vsc, lo, hi, scale, int(num_splits),
-                              (out.dtype if out is not None else out_dtype) == torch.float32)
-    return res if out is None else out.copy_(res)
+    if out is None:
+        return ops.attention_fp8kv(q, kc, vc, ksc, vsc, lo, hi, scale, int(num_splits),
+                                   out_dtype == torch.float32, dlo, dhi)
+    if out.dtype not in (torch.bfloat16, torch.float32) or out.shape != q.shape:
+        raise ValueError("out must be a bf16 or fp32 tensor of q's shape")
+    ops.attention_fp8kv_out(q, kc, vc, ksc, vsc, lo, hi, scale, int(num_splits), out, dlo, dhi)
+    return out

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
     for name in _header_functions():
         assert hasattr(lib, name), name
     lib.lbw_abi_version.restype = ctypes.c_int
-    assert lib.lbw_abi_version() == 2
+    assert lib.lbw_abi_version() == 3
 
 
 def _header_struct_fields(name):
@@ -62,6 +62,71 @@ def test_ctypes_structs_match_header(cname, pyname):
     from lbw_amd import _lib
     py = [f[0] for f in getattr(_lib, pyname)._fields_]
     assert py == _header_struct_fields(cname)
+
+
+_CTYPE = {"int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64, "float": ctypes.c_float}
+
+
+def _header_struct(name, known):
+    """A ctypes struct built from the header's own declaration of `name` (pointers as
+    c_void_p, `T x[N]` as arrays, nested structs from `known`), for layout comparisons."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    consts = dict(re.findall(r"#define (LBW_[A-Z_]+) (\d+)\b", text))
+    m = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S)
+    assert m, name
+    fields = []
+    for decl in m.group(1).split(";"):
+        decl = " ".join(decl.split())
+        if not decl:
+            continue
+        decl = decl.replace("const ", "")
+        base, rest = decl.split(" ", 1)
+        for item in rest.split(","):
+            item = item.strip()
+            ptr = base.endswith("*") or item.startswith("*")
+            item = item.lstrip("*").strip()
+            arr = re.match(r"(\w+)\[(\w+)\]", item)
+            fname = arr.group(1) if arr else item
+            t = ctypes.c_void_p if ptr else (known[base] if base in known else _CTYPE[base])
+            if arr:
+                n = arr.group(2)
+                t = t * int(consts.get(n, n))
+            fields.append((fname, t))
+    return type(name, (ctypes.Structure,), {"_fields_": fields})
+
+
+def _integration_stub():
+    """The Seg and Params classes of the ctypes stub in INTEGRATION.md, executed as written."""
+    import ast
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
+    block = next(b for b in blocks if "class Params(ctypes.Structure)" in b)
+    tree = ast.parse(block)
+    classes = [n for n in tree.body if isinstance(n, ast.ClassDef)]
+    ns = {"ctypes": ctypes}
+    exec(compile(ast.Module(body=classes, type_ignores=[]), "INTEGRATION.md", "exec"), ns)
+    return ns["Seg"], ns["Params"]
+
+
+def _layout(struct):
+    return [(f[0], getattr(struct, f[0]).offset, getattr(struct, f[0]).size)
+            for f in struct._fields_]
+
+
+def test_integration_stub_matches_header():
+    """The binding INTEGRATION.md shows a maintainer has every field of the header's structs,
+    in order, at the same offsets and sizes: a stub missing a trailing field would let the
+    library read past the caller's struct."""
+    seg_h = _header_struct("lbw_kv_segment", {})
+    par_h = _header_struct("lbw_attn_params", {"lbw_kv_segment": seg_h})
+    seg_d, par_d = _integration_stub()
+    assert _layout(seg_d) == _layout(seg_h)
+    assert _layout(par_d) == _layout(par_h)
+    assert ctypes.sizeof(par_d) == ctypes.sizeof(par_h)
+    from lbw_amd import _lib
+    assert _layout(_lib.AttnParams) == _layout(par_h)
+    assert "lbw_abi_version() == %d" % _lib.ABI_VERSION in open(os.path.join(ROOT, "INTEGRATION.md")).read()
 
 
 def test_entry_points_reject_bad_arguments_without_gpu():
@@ -208,9 +273,9 @@ def test_torch_op_set_registers_with_shapes():
     import torch
     from lbw_amd import _lib
     ops = _lib.ops()
-    for name in ("attention", "attention_out", "cross_attention", "attention_fp8kv",
-                 "attention_partial", "attention_merge", "attention_merge_out", "qk_norm_rope_",
-                 "kv_quant_fp8_"):
+    for name in ("attention", "attention_out", "cross_attention", "cross_attention_out",
+                 "attention_fp8kv", "attention_fp8kv_out", "attention_partial",
+                 "attention_merge", "attention_merge_out", "qk_norm_rope_", "kv_quant_fp8_"):
         assert hasattr(ops, name), name
     q = torch.empty(2, 10, 3, 128, dtype=torch.bfloat16, device="meta")
     k = torch.empty(2, 70, 3, 128, dtype=torch.bfloat16, device="meta")
@@ -224,3 +289,9 @@ def test_torch_op_set_registers_with_shapes():
     c8 = torch.empty(2, 70, 3, 128, dtype=torch.uint8, device="meta")
     s8 = torch.empty(2, 3, 2, dtype=torch.float32, device="meta")
     assert ops.attention_fp8kv(q, [c8], [c8], [s8], [s8], 0, -1, 0.0, 0, False).shape == q.shape
+    # the window as device tensors (one-element int64, read by the kernel)
+    lo = torch.empty(1, dtype=torch.int64, device="meta")
+    assert ops.attention(q, [k], [k], 0, -1, None, 0.0, 0, False, lo, lo).shape == q.shape
+    assert ops.attention(q, [k], [k], kv_lo_dev=lo, kv_hi_dev=lo).shape == q.shape
+    assert ops.attention_partial(q, [k], [k], 0, -1, 0.0, lo, lo)[0].shape == (2, 3, 10, 128)
+    assert ops.attention_fp8kv(q, [c8], [c8], [s8], [s8], kv_hi_dev=lo).shape == q.shape

@@ -255,6 +255,34 @@ def test_torch_ops_refuse_wrong_types_and_shapes(lib):
         ops.qk_norm_rope_(x, None, None, None, w, None, rope, dims, 1e-6, 2,
                           torch.zeros(2, 128, L, dtype=torch.bfloat16, device=DEV)[:, :, :4],
                           None, None, None, 1.0, 1.0, 1)
+    # RoPE tables shorter than the grid's (f, h, w, s0, s1) need
+    with pytest.raises(RuntimeError, match="rope holds"):
+        ops.qk_norm_rope_(x, None, None, None, w, None, torch.zeros(100, device=DEV),
+                          [1, 2, 4, 22, 21], 1e-6, 2, x.clone(), None, None, None, 1.0, 1.0, 0)
+    # quantiser scales of the wrong size or device
+    xq = torch.zeros(1, 130, 2, 128, dtype=torch.bfloat16, device=DEV)
+    c8 = torch.zeros(1, 130, 2, 128, dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError, match="scales must be"):
+        ops.kv_quant_fp8_(xq, c8, torch.zeros(1, 2, 2, device=DEV))
+    with pytest.raises(RuntimeError, match="device"):
+        ops.kv_quant_fp8_(xq, c8, torch.zeros(1, 2, 3))
+    # merge partials whose (B, N) differ from O's, or that sit on another device
+    po = torch.zeros(1, 2, 8, 128, device=DEV)
+    pm = torch.zeros(1, 2, 8, device=DEV)
+    ob = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="differ in shape"):
+        ops.attention_merge_out([po], [torch.zeros(1, 3, 8, device=DEV)],
+                                [torch.zeros(1, 3, 8, device=DEV)], ob)
+    with pytest.raises(RuntimeError, match="device"):
+        ops.attention_merge_out([po], [pm.cpu()], [pm], ob)
+    # device window bounds that are not one-element integer tensors on q's device
+    kq = torch.zeros(1, 16, 2, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match="kv_hi_dev"):
+        ops.attention(q, [kq], [kq], 0, -1, None, 0.0, 0, False, None,
+                      torch.tensor([3.0], device=DEV))
+    with pytest.raises(RuntimeError, match="kv_lo_dev"):
+        ops.attention(q, [kq], [kq], 0, -1, None, 0.0, 0, False,
+                      torch.tensor([1, 2], device=DEV), None)
     torch.cuda.synchronize()
 
 
