@@ -40,6 +40,8 @@ struct AttnKernelArgs {
   int B, H, Lq;
   int n_qtiles, splits;
   uint32_t* queue;    // 8 work-queue counters (zeroed before the launch), or null: static order
+  uint32_t* merge_cnt;  // split partials merged in-kernel: one arrival counter per unit (zeroed
+                        // with the queue counters, right after them); null: a separate merge
   int mode;
   float* part_o;
   float* part_m;

@@ -164,8 +164,74 @@ __device__ __forceinline__ int take_item(uint32_t* q, uint32_t U, uint32_t S, ui
   return -1;
 }
 
-__global__ void __launch_bounds__(64) attn_queue_reset_kernel(uint32_t* q) {
-  if (threadIdx.x < 8) q[threadIdx.x] = 0u;
+__global__ void __launch_bounds__(256) attn_queue_reset_kernel(uint32_t* q, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) q[i] = 0u;
+}
+
+// Stores and loads of the split partials when the last piece of a unit merges them: at device
+// scope (sc1), so that they reach, and are read from, the point where the XCDs' caches are
+// coherent; the XCD's own L2 holds no line of them that another XCD could miss.
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int kDevScope = 16;  // buffer cache-policy bit sc1: device scope
+
+// The log-sum-exp merge of the N split partials of one unit's `rows` rows (the
+// attn_merge_kernel arithmetic, which it must match bit for bit), by the workgroup of the
+// unit's last piece. `wl` is LDS scratch for N x 256 weights and 256 reciprocals.
+template <int N>
+__device__ void merge_unit(const AttnKernelArgs& a, int b, int h, int qt, int rows, float* wl) {
+  const int64_t per = (int64_t)a.B * a.H * a.Lq;          // rows of one split
+  const int64_t base = ((int64_t)b * a.H + h) * a.Lq + (int64_t)qt * BM;
+  float* inv = wl + 16 * BM;
+  for (int r = threadIdx.x; r < rows; r += NWAVE * 64) {
+    float ms[N], ls[N];
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+      ms[s] = load_dev(a.part_m + s * per + base + r);
+      ls[s] = load_dev(a.part_l + s * per + base + r);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < N; ++s) M = fmaxf(M, ms[s]);
+    float den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < N; ++s) {
+      const float w = (M == -INFINITY || ms[s] == -INFINITY) ? 0.0f : expf(ms[s] - M);
+      den += w * ls[s];
+      wl[s * BM + r] = w;
+    }
+    inv[r] = den > 0.0f ? 1.0f / den : 0.0f;
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.part_o + base * D), (short)0, 0x7fffffff, 0x00020000);
+  const uint32_t sstride = (uint32_t)(per * D * 4);  // bytes between splits
+  for (int c = threadIdx.x; c < rows * (D / 4); c += NWAVE * 64) {
+    const int r = c / (D / 4), dq = c % (D / 4);
+    floatx4 os[N];
+#pragma unroll
+    for (int s = 0; s < N; ++s)
+      os[s] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+          rp, (uint32_t)(r * D + 4 * dq) * 4u, s * sstride, kDevScope));
+    floatx4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < N; ++s) num += wl[s * BM + r] * os[s];
+    const float iv = inv[r];
+    const int q = qt * BM + r;
+    const int64_t off = a.osb * b + a.osl * (int64_t)q + a.osh * h + 4 * dq;
+    if (a.o32) {
+      *reinterpret_cast<floatx4*>(reinterpret_cast<float*>(a.out) + off) = num * iv;
+    } else {
+      u32x2 w;
+      w[0] = pack_bf16x2(num[0] * iv, num[1] * iv);
+      w[1] = pack_bf16x2(num[2] * iv, num[3] * iv);
+      *reinterpret_cast<u32x2*>(a.out + off) = w;
+    }
+  }
 }
 
 // FP8 = false: bf16 K/V, DMA'd straight into LDS. FP8 = true: e4m3 K/V codes with fp32 scales
@@ -697,6 +763,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
+        if (i + V_AHEAD < 8) load_v(voff_c, i + V_AHEAD);
+        else if constexpr (NVO >= 0) load_v(nvo_c, i + V_AHEAD - 8);
         if constexpr (FP8) {
           // K of d-half 1 at once; the next step's d-half 0 once this step's last use of it
           // (the lo product at i = 2) is issued
@@ -707,8 +775,6 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           if (i + K_AHEAD < 8) load_k(koff_c, i + K_AHEAD);
           else if constexpr (NKO >= 0) load_k(nko_c, i + K_AHEAD - 8);
         }
-        if (i + V_AHEAD < 8) load_v(voff_c, i + V_AHEAD);
-        else if constexpr (NVO >= 0) load_v(nvo_c, i + V_AHEAD - 8);
         if constexpr (FP8) {
           // QK on the fp8 cores at even i: (d-half i / 4) x (hi, lo)
           if ((i & 1) == 0) {
@@ -802,8 +868,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           if (mlim > 0.0f) {
             d = fmaxf(mx, 0.0f);
             alpha = fast_exp2(-d);
-            // O (with this step's PV of the previous sub-block, at the old reference) moves now
+            // O (with this step's PV of the previous sub-block, at the old reference) and the
+            // row sum move now
             scale_acc(oacc, alpha);
+            lsum *= alpha;
           } else {
             const bool set = mx > -INFINITY;  // a fully masked sub-block leaves it unset
             d = set ? mx : 0.0f;
@@ -838,12 +906,17 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           m_used = m_new;
           move = true;
           ca = lsv - m_new * c;
-          // O (with this step's PV of the previous sub-block, at the old reference) moves now
+          // O (with this step's PV of the previous sub-block, at the old reference) and the
+          // row sum move now
           scale_acc(oacc, alpha);
+          lsum *= alpha;
           ls = exps();
         }
       }
-      lsum = __builtin_fmaf(lsum, alpha, ls);
+      // (TRACK decided its move before the exponentials; the other forms rescaled lsum in the
+      // redo branch, so their common path is one add)
+      if constexpr (TRACK) lsum = __builtin_fmaf(lsum, alpha, ls);
+      else lsum += ls;
       // keep the exponentials in this step's block (not sunk into the next one)
       asm volatile("" ::"v"(p_out[0]), "v"(p_out[1]), "v"(lsum));
       pend = TRACK && move;  // (the other forms have rescaled O in the redo branch)
@@ -932,7 +1005,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
   // Every wave is past its last LDS reads (the drain) before the LDS is reused for staging O.
   barrier_nofence();
-  if (!wave_active) return;
+  // (with the in-kernel merge every wave stays for the unit's arrival count)
+  const bool fused = a.mode == kModePartials && a.merge_cnt != nullptr;
+  if (!wave_active && !fused) return;
 
   // ---- epilogue
   // (a workgroup with no tiles still has its Q loads outstanding)
@@ -970,7 +1045,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         }
       }
     }
-  } else {
+  } else if (wave_active) {
     // fp32 rows: the normalised output of an fp32-output call, or the partials.
     // cte_partial contract (TRACK): O and l relative to the true row max, m in scaled units;
     // the split-KV partials for lbw's own merge keep the exponent reference instead.
@@ -992,9 +1067,16 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     const int64_t row0 = ((int64_t)(split * a.B + b) * a.H + h) * a.Lq;
     const int q = q0 + l32;
     if (!norm32 && q < a.Lq && hl == 0) {
-      a.part_m[row0 + q] = m_out;
-      a.part_l[row0 + q] = l_tot * f;
+      if (fused) {
+        store_dev(a.part_m + row0 + q, m_out);
+        store_dev(a.part_l + row0 + q, l_tot * f);
+      } else {
+        a.part_m[row0 + q] = m_out;
+        a.part_l[row0 + q] = l_tot * f;
+      }
     }
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.part_o + row0 * D), (short)0, 0x7fffffff, 0x00020000);
     float* const out32 = reinterpret_cast<float*>(a.out) + a.osb * b + a.osh * h;
     // fp32 O in two halves of 64 d (256 B per row each)
 #pragma unroll
@@ -1018,10 +1100,40 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         const floatx4 v = *reinterpret_cast<const floatx4*>(stg + r * 256 + ((rch ^ (r & 15)) << 4));
         const int qq = q0 + r;
         if (qq < a.Lq) {
-          float* dst = norm32 ? out32 + a.osl * (int64_t)qq : a.part_o + (row0 + qq) * D;
-          *reinterpret_cast<floatx4*>(dst + 64 * half + 4 * rch) = v;
+          if (fused) {
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
+                                                   (uint32_t)(qq * D + 64 * half + 4 * rch) * 4u,
+                                                   0, kDevScope);
+          } else {
+            float* dst = norm32 ? out32 + a.osl * (int64_t)qq : a.part_o + (row0 + qq) * D;
+            *reinterpret_cast<floatx4*>(dst + 64 * half + 4 * rch) = v;
+          }
         }
       }
+    }
+  }
+  if (fused) {
+    // The last piece of the unit to arrive merges the unit's partials: every store of this
+    // workgroup is complete at device scope before its one arrival is counted, and the last
+    // arrival reads the others' partials at device scope after its count returned.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __shared__ int s_last;
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(a.merge_cnt + unit, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)a.splits - 1u;
+    __syncthreads();
+    if (!s_last) return;
+    const int rows = min(BM, a.Lq - qt * BM);
+    float* wl = reinterpret_cast<float*>(lds + V_BASE);
+    switch (a.splits) {
+      case 2: merge_unit<2>(a, b, h, qt, rows, wl); break;
+      case 3: merge_unit<3>(a, b, h, qt, rows, wl); break;
+      case 4: merge_unit<4>(a, b, h, qt, rows, wl); break;
+      case 5: merge_unit<5>(a, b, h, qt, rows, wl); break;
+      case 6: merge_unit<6>(a, b, h, qt, rows, wl); break;
+      case 7: merge_unit<7>(a, b, h, qt, rows, wl); break;
+      default: merge_unit<8>(a, b, h, qt, rows, wl); break;
     }
   }
 }
@@ -1040,7 +1152,10 @@ static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
     // spare workgroups, 1/16 of an XCD's share (at least one each): enough for the measured
     // spread of XCD speeds (a few percent)
     nwg += 8u * ((per_xcd + 15u) / 16u);
-    hipLaunchKernelGGL(attn_queue_reset_kernel, dim3(1), dim3(64), 0, stream, a.queue);
+    // the 8 queue counters and, for the in-kernel merge, the U arrival counters after them
+    const int n = 8 + (a.merge_cnt != nullptr ? (int)U : 0);
+    hipLaunchKernelGGL(attn_queue_reset_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64),
+                       dim3(256), 0, stream, a.queue, n);
   }
   hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
                      stream, a);

@@ -114,9 +114,14 @@ int choose_splits(int64_t bh, int lq, int bm, int64_t ntiles, int cus) {
 
 constexpr size_t kQueueBytes = 256;  // 8 work-queue counters, padded
 
+// Split calls of up to this many pieces merge their partials in the attention kernel (the last
+// piece of each unit); more pieces run the separate merge kernel.
+constexpr int kMaxFusedSplits = 8;
+
 struct Plan {
   AttnKernelArgs a;
   int splits;
+  bool fused_merge;   // the pieces merge in-kernel (no merge launch)
   size_t part_bytes;  // split partials
   size_t queue_off;   // work-queue counters
   size_t ws_bytes;
@@ -225,10 +230,14 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
     }
   }
   plan->splits = splits;
-  // [split partials][work-queue counters at a 256-byte boundary]
+  // [split partials][8 work-queue counters at a 256-byte boundary, then (split calls whose
+  // pieces merge in-kernel) one arrival counter per unit]
   plan->part_bytes = splits > 1 ? (size_t)splits * a.B * a.H * a.Lq * (p->head_dim + 2) * sizeof(float) : 0;
   plan->queue_off = (plan->part_bytes + 255) & ~(size_t)255;
-  plan->ws_bytes = plan->queue_off + kQueueBytes;
+  plan->fused_merge = splits > 1 && splits <= kMaxFusedSplits;
+  const size_t units = (size_t)a.n_qtiles * a.H * a.B;
+  const size_t cnt_bytes = (8 + (plan->fused_merge ? units : 0)) * sizeof(uint32_t);
+  plan->ws_bytes = plan->queue_off + std::max(kQueueBytes, (cnt_bytes + 255) & ~(size_t)255);
   a.splits = splits;
   return LBW_OK;
 }
@@ -278,10 +287,11 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
     a.part_m = base + rows * p->head_dim;
     a.part_l = a.part_m + rows;
     a.mode = kModePartials;
+    if (plan.fused_merge) a.merge_cnt = a.queue + 8;
   }
   hipError_t e = fp8 ? launch_attn_fwd_fp8(a, st) : launch_attn_fwd(a, st);
   if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
-  if (plan.splits > 1) {
+  if (plan.splits > 1 && !plan.fused_merge) {
     MergeKernelArgs m;
     memset(&m, 0, sizeof(m));
     m.n = plan.splits;
@@ -420,8 +430,11 @@ int lbw_attention_fwd_noalloc(const lbw_attn_params* p, void* stream) {
                   "(ask for fewer splits, 0 = the most that fit, or use lbw_attention_fwd)",
                   p->num_splits, plan.ws_bytes, (size_t)LBW_NOALLOC_SCRATCH_BYTES);
     // the host's choice does not fit: the largest split count whose partials do (1 always does)
+    // next to the counters (8 + one per unit) and the alignment gap
     const size_t per = (size_t)p->batch * p->heads * p->lq * (p->head_dim + 2) * sizeof(float);
-    const size_t room = LBW_NOALLOC_SCRATCH_BYTES - 512;
+    const size_t units = (size_t)plan.a.n_qtiles * p->heads * p->batch;
+    const size_t fixed = 512 + (8 + units) * sizeof(uint32_t);
+    const size_t room = LBW_NOALLOC_SCRATCH_BYTES > fixed ? LBW_NOALLOC_SCRATCH_BYTES - fixed : 0;
     q.num_splits = (int)std::max<size_t>(1, std::min<size_t>(plan.splits - 1, room / per));
   }
   void* ws = noalloc_scratch();

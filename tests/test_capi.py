@@ -195,7 +195,9 @@ def _split_count(H, LQ, LK):
 
 def test_workspace_layout_without_gpu():
     """Workspace = split partials (splits x rows x (D + 2) fp32) rounded up to 256 bytes, then
-    256 bytes of work-queue counters; a single-pass plan needs only the counters."""
+    the counters: 8 work-queue counters and, for a split plan (its pieces merge in the kernel),
+    one arrival counter per (batch, head, 256-query tile), rounded up to 256 bytes (at least
+    256); a single-pass plan needs only the queue counters."""
     from lbw_amd import _lib
     lib = _lib.load()
     for H, LQ, LK in [(2, 256, 1024), (40, 3600, 46800), (40, 4680, 32760), (12, 4680, 14040)]:
@@ -216,7 +218,10 @@ def test_workspace_layout_without_gpu():
         n = lib.lbw_attention_workspace_size(ctypes.byref(p))
         splits = _split_count(H, LQ, LK)
         parts = splits * LQ * H * 130 * 4 if splits > 1 else 0
-        assert n == ((parts + 255) // 256) * 256 + 256, (H, LQ, LK, n, splits)
+        units = H * ((LQ + 255) // 256)
+        cnt = 4 * (8 + (units if splits > 1 else 0))
+        assert n == ((parts + 255) // 256) * 256 + max(256, (cnt + 255) // 256 * 256), \
+            (H, LQ, LK, n, splits)
 
 
 def test_segment_length_limit_without_gpu():

@@ -374,3 +374,24 @@ def test_cross_attention_dedup_matches_full_context():
     assert nd2 == 95
     out2 = cross_attention(q.to(DEV), k2.to(DEV), v2.to(DEV), n_distinct=nd2)
     assert_parity(out2, O.attention_ref(q, k2, v2), "dedup, no padding")
+
+
+@pytest.mark.parametrize("splits", [2, 3, 5, 8, 9, 12])
+def test_split_pieces_merged_in_kernel(lib, splits):
+    """Split calls of up to 8 pieces merge in the attention kernel (the last piece of each
+    (batch, head, q-tile) unit to finish reads the others' partials at device scope); more
+    pieces run the separate merge kernel. Many units spread over the XCDs: parity with the
+    oracle, bf16 output = the fp32 output rounded once, and repeated calls bit for bit equal."""
+    from lbw_amd import attention_segments
+    q, ks, vs = _case(3, 1000, 16, [1500, 700], seed=splits, gain=False)
+    segs = [(k.to(DEV), v.to(DEV)) for k, v in zip(ks, vs)]
+    qd = q.to(DEV)
+    runs = [attention_segments(qd, segs, num_splits=splits) for _ in range(3)]
+    o32 = attention_segments(qd, segs, num_splits=splits, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1))
+    print(f"splits={splits}", metrics(runs[0], ref), flush=True)
+    assert_parity(runs[0], ref)
+    for r in runs[1:]:
+        assert torch.equal(r, runs[0])
+    assert torch.equal(o32.to(torch.bfloat16), runs[0])
