@@ -100,14 +100,27 @@ def test_fp8_full_size_long_horizon(lib):
         s = torch.where(torch.rand(x.shape, generator=gd, device=DEV) < 0.5, -8.0, 8.0)
         return torch.where(m, s, x).to(torch.bfloat16)
     k, v = kv(), kv()
-    out = attention_fp8kv(q, [(quantize_kv_fp8(k), quantize_kv_fp8(v))])
+    kq, vq = quantize_kv_fp8(k), quantize_kv_fp8(v)
+    out = attention_fp8kv(q, [(kq, vq)])
     torch.cuda.synchronize()
     sel = torch.randperm(Lq, generator=torch.Generator().manual_seed(1))[:128].sort().values
     for h in (0, 23):
         ref = O.attention_ref(q[:, sel, h:h + 1].cpu(), k[:, :, h:h + 1].cpu(), v[:, :, h:h + 1].cpu())
         c = cosine(out[:, sel, h:h + 1], ref)
-        print(f"fp8 full size head {h}: cosine {c:.6f}")
+        # max-abs beside the cosine: the quantised cache alone moves the output by what the
+        # oracle on the dequantised K/V shows; the kernel may add its bf16 tolerance on top
+        kd = O.dequantize_kv_fp8(kq.codes[:, :, h:h + 1].cpu(), kq.scales[:, h:h + 1].cpu())
+        vd = O.dequantize_kv_fp8(vq.codes[:, :, h:h + 1].cpu(), vq.scales[:, h:h + 1].cpu())
+        ref_d = O.attention_ref(q[:, sel, h:h + 1].cpu(), kd, vd)
+        quant = float((ref_d - ref).abs().max())
+        m = metrics(out[:, sel, h:h + 1], ref)
+        md = metrics(out[:, sel, h:h + 1], ref_d)
+        print(f"fp8 full size head {h}: cosine {c:.6f}, max-abs {m['max_abs']:.4f} vs the fp32 "
+              f"reference (quantisation alone {quant:.4f}), {md['max_abs']:.4f} vs the "
+              f"dequantised-cache reference")
         assert c >= FP8_COSINE
+        assert md["max_abs"] <= 1e-2
+        assert m["max_abs"] <= quant + 1e-2
 
 
 def _wide_q(Lq, H, g):
