@@ -114,30 +114,106 @@ def _cpu_model() -> str:
     return f"{name} ({os.cpu_count()} logical CPUs visible)"
 
 
-def cpu_baseline(budget_s: float = 12.0):
-    """The oracle on the host cores: fp32 attention of the same workload, one head at a time
-    until the time budget is used, scaled to TFLOP/s."""
+def _cpu_attention_heads(g, heads, lq, lk, budget_s, fp8=False, valid=None):
+    """The oracle's fp32 attention of `heads` heads (lq queries over lk keys, bf16 inputs), one
+    head at a time until `budget_s` is used; with `fp8` the keys and values go through the
+    oracle's e4m3 quantiser and are dequantised first (what the fp8 cache holds); `valid`
+    masks the keys to a valid length (the masked cross-attention). Returns (heads done, s)."""
     import torch
     import oracle as O
+    done, spent = 0, 0.0
+    kl = None if valid is None else torch.tensor([valid], dtype=torch.int32)
+    while done < heads:
+        q = torch.randn(1, lq, 1, D, generator=g).to(torch.bfloat16)
+        k = torch.randn(1, lk, 1, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, lk, 1, D, generator=g).to(torch.bfloat16)
+        if fp8:   # (the quantiser is not timed: the attention reads the dequantised cache)
+            k = O.dequantize_kv_fp8(*O.quantize_kv_fp8(k.float()))
+            v = O.dequantize_kv_fp8(*O.quantize_kv_fp8(v.float()))
+        t0 = time.perf_counter()
+        O.attention_ref(q, k, v, k_lens=kl, q_block=600)
+        spent += time.perf_counter() - t0
+        done += 1
+        if spent >= budget_s:
+            break
+    return done, spent
+
+
+def _cpu_qk_norm_rope(g, lq, grid, start_frame, heads):
+    """The oracle's q/k RMSNorm + 3-D RoPE (qk_post arithmetic) of one chunk, q and k, in
+    seconds."""
+    import torch
+    import oracle as O
+    C = heads * D
+    xq = torch.randn(lq, C, generator=g).to(torch.bfloat16)
+    xk = torch.randn(lq, C, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16)
+    t0 = time.perf_counter()
+    cos, sin = O.causal_rope_grids(O.wan_rope_freqs(D), *grid, start_frame=start_frame)
+    O.qk_post_norm_rope(xq, None, w, cos, sin)
+    O.qk_post_norm_rope(xk, None, w, cos, sin)
+    return time.perf_counter() - t0
+
+
+def _cpu_c1_layer(g):
+    """One whole Wan-1.3B self-attention layer in fp32 on the host (the oracle's layer: QKV
+    projections, RMSNorm, 3-D RoPE, attention over 2 cached frames + the chunk, o-projection),
+    480p, one latent frame of 1560 tokens; seconds and FLOP."""
+    import torch
+    import oracle as O
+    C1, H1, grid = 1536, 12, (1, 30, 52)
+    L = grid[1] * grid[2]
+    rn = lambda *s, sc=1.0: (sc * torch.randn(*s, generator=g))
+    x, xc = rn(1, L, C1), rn(1, 2 * L, C1)
+    w = [rn(C1, C1, sc=0.02) for _ in range(4)]
+    b = [rn(C1, sc=0.02) for _ in range(4)]
+    gq, gk = 1 + 0.1 * rn(C1), 1 + 0.1 * rn(C1)
+    t0 = time.perf_counter()
+    O.self_attention_layer_ref(x, xc, w[0], b[0], w[1], b[1], w[2], b[2], w[3], b[3], gq, gk,
+                               heads=H1, grid=grid, cache_grid=(2, 30, 52), start_frame=2)
+    dt = time.perf_counter() - t0
+    flops = 2.0 * L * C1 * C1 * 4 + 2.0 * 2 * L * C1 * C1 * 2 + 4.0 * L * 3 * L * (C1 // H1) * H1
+    return dt, flops
+
+
+def cpu_baseline(budget_s: float = 12.0):
+    """The oracle on the host cores: fp32 attention of the same workload (the 14B 720p chunk),
+    one head at a time until the time budget is used, scaled to TFLOP/s; and, under
+    ``per_config``, every other workload of the path on a bounded sample (whole c1 layer;
+    attention and q/k norm + RoPE per layer at the 1.3B / 14B 480p chunks, the cross-attention
+    and the fp8-cache long horizon), each extrapolated to one layer."""
+    import torch
     torch.set_num_threads(os.cpu_count() or 1)
     g = torch.Generator().manual_seed(7)
-    heads = 0
-    t0 = time.perf_counter()
-    while heads < H:
-        q = torch.randn(1, LQ, 1, D, generator=g).to(torch.bfloat16)
-        k = torch.randn(1, LK, 1, D, generator=g).to(torch.bfloat16)
-        v = torch.randn(1, LK, 1, D, generator=g).to(torch.bfloat16)
-        O.attention_ref(q, k, v, q_block=600)
-        heads += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = time.perf_counter() - t0
+    heads, dt = _cpu_attention_heads(g, H, LQ, LK, budget_s)
     flops = 4.0 * LQ * LK * D * heads
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
-            "cpu_model": _cpu_model(), "kind": "port",
-            "sample": f"oracle fp32 attention, {heads} of {H} heads of one layer "
-                      f"({LQ} q x {LK} k x {D}), {dt:.1f} s; "
-                      f"ms per 40-layer chunk extrapolated: {dt / heads * H * 40 * 1e3:.0f}"}
+    res = {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+           "cpu_model": _cpu_model(), "kind": "port",
+           "sample": f"oracle fp32 attention, {heads} of {H} heads of one layer "
+                     f"({LQ} q x {LK} k x {D}), {dt:.1f} s; "
+                     f"ms per 40-layer chunk extrapolated: {dt / heads * H * 40 * 1e3:.0f}"}
+    per = {}
+    t, fl = _cpu_c1_layer(g)
+    per["wan13b_480p_1f_over_2f_full_layer"] = {
+        "ms_per_layer": round(t * 1e3, 1), "TFLOP/s": round(fl / t / 1e12, 4),
+        "sample": "whole layer (projections, norm, RoPE, attention, o-projection), fp32"}
+    for name, h, lq, lk, grid, sf, kw in (
+            ("wan13b_480p_3f_over_6f", 12, 4680, 14040, (3, 30, 52), 6, {}),
+            ("wan14b_480p_3f_over_18f", 40, 4680, 32760, (3, 30, 52), 18, {}),
+            ("wan14b_480p_cross_512ctx_300valid", 40, 4680, 512, None, 0, {"valid": 300}),
+            ("wan14b_480p_cross_512ctx_unmasked", 40, 4680, 512, None, 0, {}),
+            ("wan14b_720p_1f_over_24f_fp8kv", 40, 3600, 90000, (1, 45, 80), 24, {"fp8": True})):
+        n, ta = _cpu_attention_heads(g, h, lq, lk, 1.5, **kw)
+        nk = kw.get("valid", lk)
+        fl = 4.0 * lq * nk * D * n
+        ent = {"attention_ms_per_layer": round(ta / n * h * 1e3, 1),
+               "attention_TFLOP/s": round(fl / ta / 1e12, 4),
+               "sample": f"{n} of {h} heads, extrapolated"}
+        if grid is not None:
+            ent["qk_norm_rope_ms_per_layer"] = round(_cpu_qk_norm_rope(g, lq, grid, sf, h) * 1e3, 1)
+        per[name] = ent
+    res["per_config"] = per
+    return res
 
 
 _SLEEP_CYCLES_PER_MS = []
@@ -588,7 +664,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": round(tr["attn_traffic_bytes"]) if tr else None,
-                     "kernel": "chunk attention call (attn_fwd_bf16_kernel + split merge)",
+                     "kernel": "chunk attention call (queue reset + attn_fwd_bf16_kernel, split pieces merged in-kernel)",
                      "flops_per_launch": flops_layer,
                      "algorithmic_bytes_per_launch": attn_bytes()},
         "qk_norm_rope_roofline": {"bound": "hbm",
