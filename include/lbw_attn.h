@@ -21,6 +21,7 @@
  *                                                              cross_attention_dedup
  *                          kernels/cross_dedup.py              cross_dedup_kernel
  *   lbw_attn_merge         wan/modules/attention.py:963-990    cte_merge
+ *   lbw_attn_merge_partials wan/modules/attention.py:654-694   cte_call's chain state
  *   lbw_qk_norm_rope       kernels/qk_post.py:404-413          qk_ss + qk_norm_rope
  *                          (caller wan/modules/model_fast.py:2596-2681 _qkv_post)
  *   lbw_kv_quant_fp8       no reference counterpart (new fp8-e4m3 KV cache)
@@ -152,6 +153,17 @@ int lbw_attn_merge(int32_t n_parts, const float* const* part_o, const float* con
                    const float* const* part_l, int32_t batch, int32_t heads, int32_t lq,
                    int32_t head_dim, void* out, int64_t o_stride_b, int64_t o_stride_l,
                    int64_t o_stride_h, void* stream);
+
+/* The same log-sum-exp merge into one partial triple instead of the normalised output: out_o
+ * [B, H, Lq, D] = sum_i e^(m_i - M) O_i, out_m [B, H, Lq] = M = max_i m_i, out_l = sum_i
+ * e^(m_i - M) l_i (all fp32, contiguous; M = -inf, O = 0, l = 0 for a row with no keys). The
+ * running (O, max, sum) state of cte_call's chain: each call's partials merged into it keep it
+ * one triple however many calls there are; lbw_attn_merge of the final triple normalises.
+ * The outputs must not overlap the inputs. */
+int lbw_attn_merge_partials(int32_t n_parts, const float* const* part_o,
+                            const float* const* part_m, const float* const* part_l, int32_t batch,
+                            int32_t heads, int32_t lq, int32_t head_dim, float* out_o,
+                            float* out_m, float* out_l, void* stream);
 
 /* Fused q/k post-processing of one chunk (kernels/qk_post.py semantics, full-row RMSNorm):
  *   y = x + b (fp32); r = rsqrt(sum(y^2)/C + eps); t = bf16(y*r) * gamma (fp32);

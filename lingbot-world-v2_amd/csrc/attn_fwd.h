@@ -61,6 +61,11 @@ struct MergeKernelArgs {
   uint16_t* out;      // bf16, or fp32 when o32
   int64_t osb, osl, osh;
   int o32;
+  // partial output (the merged (O, m, l) triple, [B, H, Lq, D] / [B, H, Lq], contiguous) instead
+  // of the normalised `out`, when part_o is set
+  float* part_o;
+  float* part_m;
+  float* part_l;
 };
 
 int attn_lds_bytes();

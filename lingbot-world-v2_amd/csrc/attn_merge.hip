@@ -3,7 +3,9 @@
 // split's row max), the row max m_s (scaled scores) and the row sum l_s,
 //   out = sum_s e^(m_s - M) O_s / sum_s e^(m_s - M) l_s,  M = max_s m_s,
 // written as bf16 (fp32 for an fp32-output call); a row whose every split is empty (all m_s =
-// -inf) yields 0.
+// -inf) yields 0. The partial form (PART) writes the merged triple instead -- O = sum_s
+// e^(m_s - M) O_s, m = M, l = sum_s e^(m_s - M) l_s -- the running (O, max, sum) state of
+// cte_call's chain (attention.py:654-694), which later calls extend and the last normalises.
 //
 // HBM-bound: per (b, h, q) row it reads n * (D + 2) fp32 values and writes D output values.
 // One thread per (row, 4 consecutive d), so every load and store is a 16 / 8-byte vector. The
@@ -14,7 +16,7 @@
 
 namespace lbw {
 
-template <int N, bool O32>
+template <int N, bool O32, bool PART = false>
 __global__ void __launch_bounds__(256)
 attn_merge_kernel(const MergeKernelArgs a) {
   const int64_t total = (int64_t)a.B * a.H * a.Lq * (a.D / 4);
@@ -47,6 +49,14 @@ attn_merge_kernel(const MergeKernelArgs a) {
         num += w * os[s];
       }
     }
+    if constexpr (PART) {
+      *reinterpret_cast<floatx4*>(a.part_o + row * a.D + 4 * dq) = num;
+      if (dq == 0) {
+        a.part_m[row] = M;
+        a.part_l[row] = den;
+      }
+      continue;
+    }
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
     const int64_t off = a.osb * b + a.osl * (int64_t)q + a.osh * h + 4 * dq;
     if constexpr (O32) {
@@ -64,12 +74,12 @@ attn_merge_kernel(const MergeKernelArgs a) {
 int attn_block_m() { return 256; }
 int attn_block_n() { return BN; }
 
-template <bool O32>
+template <bool O32, bool PART>
 static hipError_t launch_merge_n(const MergeKernelArgs& a, dim3 grid, dim3 block,
                                  hipStream_t stream) {
   switch (a.n) {
 #define LBW_MERGE_CASE(n) \
-    case n: hipLaunchKernelGGL((attn_merge_kernel<n, O32>), grid, block, 0, stream, a); break;
+    case n: hipLaunchKernelGGL((attn_merge_kernel<n, O32, PART>), grid, block, 0, stream, a); break;
     LBW_MERGE_CASE(1) LBW_MERGE_CASE(2) LBW_MERGE_CASE(3) LBW_MERGE_CASE(4)
     LBW_MERGE_CASE(5) LBW_MERGE_CASE(6) LBW_MERGE_CASE(7) LBW_MERGE_CASE(8)
     LBW_MERGE_CASE(9) LBW_MERGE_CASE(10) LBW_MERGE_CASE(11) LBW_MERGE_CASE(12)
@@ -86,8 +96,9 @@ hipError_t launch_attn_merge(const MergeKernelArgs& a, hipStream_t stream) {
   if (blocks > 65536) blocks = 65536;
   if (blocks < 1) blocks = 1;
   const dim3 grid((uint32_t)blocks), block(256);
-  return a.o32 ? launch_merge_n<true>(a, grid, block, stream)
-               : launch_merge_n<false>(a, grid, block, stream);
+  if (a.part_o != nullptr) return launch_merge_n<false, true>(a, grid, block, stream);
+  return a.o32 ? launch_merge_n<true, false>(a, grid, block, stream)
+               : launch_merge_n<false, false>(a, grid, block, stream);
 }
 
 }  // namespace lbw

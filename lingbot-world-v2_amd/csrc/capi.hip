@@ -478,6 +478,34 @@ int lbw_attn_merge(int32_t n_parts, const float* const* part_o, const float* con
   return LBW_OK;
 }
 
+int lbw_attn_merge_partials(int32_t n_parts, const float* const* part_o,
+                            const float* const* part_m, const float* const* part_l, int32_t batch,
+                            int32_t heads, int32_t lq, int32_t head_dim, float* out_o,
+                            float* out_m, float* out_l, void* stream) {
+  if (n_parts < 1 || n_parts > 16) return fail(LBW_ERR_INVALID, "n_parts %d not in [1, 16]", n_parts);
+  if (head_dim != 128) return fail(LBW_ERR_UNSUPPORTED, "head_dim %d: only 128", head_dim);
+  if (batch < 1 || heads < 1 || lq < 0) return fail(LBW_ERR_INVALID, "bad sizes");
+  if (part_o == nullptr || part_m == nullptr || part_l == nullptr || out_o == nullptr ||
+      out_m == nullptr || out_l == nullptr || !aligned16(out_o))
+    return fail(LBW_ERR_INVALID, "NULL or misaligned pointer");
+  if (lq == 0) return LBW_OK;
+  MergeKernelArgs m;
+  memset(&m, 0, sizeof(m));
+  m.n = n_parts;
+  for (int i = 0; i < n_parts; ++i) {
+    if (part_o[i] == nullptr || part_m[i] == nullptr || part_l[i] == nullptr || !aligned16(part_o[i]))
+      return fail(LBW_ERR_INVALID, "partial %d: NULL or misaligned pointer", i);
+    m.o[i] = part_o[i];
+    m.m[i] = part_m[i];
+    m.l[i] = part_l[i];
+  }
+  m.B = batch; m.H = heads; m.Lq = lq; m.D = head_dim;
+  m.part_o = out_o; m.part_m = out_m; m.part_l = out_l;
+  hipError_t e = launch_attn_merge(m, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
+  return LBW_OK;
+}
+
 int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream) {
   if (p == nullptr) return fail(LBW_ERR_INVALID, "params is NULL");
   if (p->tokens < 0 || p->heads < 1 || p->dim < 8 || p->dim % p->heads != 0)

@@ -289,6 +289,39 @@ void attention_merge_out(at::TensorList o, at::TensorList m, at::TensorList l,
         "lbw_attn_merge");
 }
 
+// The partials of (O, m, l) merged into one triple (cte_call's running chain state).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> attention_merge_partials(at::TensorList o,
+                                                                       at::TensorList m,
+                                                                       at::TensorList l) {
+  TORCH_CHECK(o.size() >= 1 && o.size() <= 16 && m.size() == o.size() && l.size() == o.size(),
+              "1..16 partials of (O, m, l)");
+  TORCH_CHECK(o[0].is_cuda() && o[0].dim() == 4, "O must be a GPU tensor [B, N, Lq, D]");
+  c10::DeviceGuard guard(o[0].device());
+  const int64_t B = o[0].size(0), H = o[0].size(1), Lq = o[0].size(2), D = o[0].size(3);
+  std::vector<const float*> po, pm, pl;
+  for (size_t i = 0; i < o.size(); ++i) {
+    TORCH_CHECK(o[i].sizes() == o[0].sizes() && m[i].dim() == 3 && m[i].size(0) == B &&
+                    m[i].size(1) == H && m[i].size(2) == Lq && l[i].sizes() == m[i].sizes(),
+                "partials differ in shape: O [B, N, Lq, D], m and l [B, N, Lq]");
+    TORCH_CHECK(o[i].device() == o[0].device() && m[i].device() == o[0].device() &&
+                    l[i].device() == o[0].device(),
+                "partials must be on one device");
+    TORCH_CHECK(o[i].is_contiguous() && m[i].is_contiguous() && l[i].is_contiguous() &&
+                    o[i].scalar_type() == at::kFloat && m[i].scalar_type() == at::kFloat &&
+                    l[i].scalar_type() == at::kFloat,
+                "partials must be contiguous fp32");
+    po.push_back(o[i].data_ptr<float>());
+    pm.push_back(m[i].data_ptr<float>());
+    pl.push_back(l[i].data_ptr<float>());
+  }
+  at::Tensor ro = at::empty_like(o[0]), rm = at::empty_like(m[0]), rl = at::empty_like(l[0]);
+  check(lbw_attn_merge_partials((int32_t)o.size(), po.data(), pm.data(), pl.data(), (int32_t)B,
+                                (int32_t)H, (int32_t)Lq, (int32_t)D, ro.data_ptr<float>(),
+                                rm.data_ptr<float>(), rl.data_ptr<float>(), stream_of(o[0])),
+        "lbw_attn_merge_partials");
+  return {ro, rm, rl};
+}
+
 at::Tensor attention_merge(at::TensorList o, at::TensorList m, at::TensorList l) {
   TORCH_CHECK(!o.empty(), "no partials");
   at::Tensor out = at::empty({o[0].size(0), o[0].size(2), o[0].size(1), o[0].size(3)},
@@ -451,6 +484,10 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> attention_partial_meta(
   auto f = q.options().dtype(at::kFloat);
   return {at::empty({B, H, Lq, D}, f), at::empty({B, H, Lq}, f), at::empty({B, H, Lq}, f)};
 }
+std::tuple<at::Tensor, at::Tensor, at::Tensor> attention_merge_partials_meta(
+    at::TensorList o, at::TensorList m, at::TensorList l) {
+  return {at::empty_like(o[0]), at::empty_like(m[0]), at::empty_like(l[0])};
+}
 at::Tensor attention_merge_meta(at::TensorList o, at::TensorList, at::TensorList) {
   return at::empty({o[0].size(0), o[0].size(2), o[0].size(1), o[0].size(3)},
                    o[0].options().dtype(at::kBFloat16));
@@ -493,6 +530,7 @@ TORCH_LIBRARY(lbw, m) {
         "float softmax_scale=0., Tensor? kv_lo_dev=None, Tensor? kv_hi_dev=None) "
         "-> (Tensor, Tensor, Tensor)");
   m.def("attention_merge(Tensor[] o, Tensor[] m, Tensor[] l) -> Tensor");
+  m.def("attention_merge_partials(Tensor[] o, Tensor[] m, Tensor[] l) -> (Tensor, Tensor, Tensor)");
   m.def("attention_merge_out(Tensor[] o, Tensor[] m, Tensor[] l, Tensor(a!) out) -> ()");
   m.def("qk_norm_rope_(Tensor q, Tensor? k, Tensor? bq, Tensor? bk, Tensor wq, Tensor? wk, "
         "Tensor rope, int[] rope_dims, float eps, int heads, Tensor(a!) q_out, "
@@ -510,6 +548,7 @@ TORCH_LIBRARY_IMPL(lbw, CUDA, m) {
   m.impl("attention_fp8kv_out", &attention_fp8kv_out);
   m.impl("attention_partial", &attention_partial);
   m.impl("attention_merge", &attention_merge);
+  m.impl("attention_merge_partials", &attention_merge_partials);
   m.impl("attention_merge_out", &attention_merge_out);
   m.impl("qk_norm_rope_", &qk_norm_rope_);
   m.impl("kv_quant_fp8_", &kv_quant_fp8_);
@@ -524,6 +563,7 @@ TORCH_LIBRARY_IMPL(lbw, Meta, m) {
   m.impl("attention_fp8kv_out", &attention_fp8kv_out_meta);
   m.impl("attention_partial", &attention_partial_meta);
   m.impl("attention_merge", &attention_merge_meta);
+  m.impl("attention_merge_partials", &attention_merge_partials_meta);
   m.impl("attention_merge_out", &attention_merge_out_meta);
   m.impl("qk_norm_rope_", &qk_norm_rope_meta);
   m.impl("kv_quant_fp8_", &kv_quant_fp8_meta);

@@ -6,7 +6,7 @@ kernels/qk_post.py, wan/modules/chunked_kv_cache.py) over the C ABI of liblbw_at
 when it is missing.
 """
 from .attention import (PRESCALED_SOFTMAX_SCALE, attention, attention_chain, attention_merge,
-                        attention_partial, attention_segments, prescaled_q_scale,
+                        attention_merge_partials, attention_partial, attention_segments, prescaled_q_scale,
                         cross_attention, exact_attention, exact_attention_chunks,
                         flash_attention, padding_start)
 from .chunked_kv_cache import (FlatKVCache, allocate_self_kv_chunks, allocate_self_kv_chunks_fp8,
@@ -19,7 +19,8 @@ from .rope import RopeTables, causal_rope_tables, rope_params, wan_rope_freqs
 
 __all__ = [
     "attention", "flash_attention", "exact_attention", "exact_attention_chunks",
-    "cross_attention", "padding_start", "attention_partial", "attention_merge", "attention_chain", "attention_segments",
+    "cross_attention", "padding_start", "attention_partial", "attention_merge",
+    "attention_merge_partials", "attention_chain", "attention_segments",
     "PRESCALED_SOFTMAX_SCALE", "prescaled_q_scale",
     "qk_norm_rope", "qk_norm_rope_", "qk_norm_rope3", "qk_norm_rope_t", "qk_norm_rope_t3",
     "x_norm_rope", "x_norm_rope_t3", "RopeTables", "causal_rope_tables", "rope_params",

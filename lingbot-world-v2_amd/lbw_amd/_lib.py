@@ -79,7 +79,8 @@ EXPORTS = (
     "lbw_attention_workspace_size", "lbw_attention_fp8kv_workspace_size", "lbw_attention_fwd",
     "lbw_cross_attention_fwd",
     "lbw_cross_attention_dedup_fwd",
-    "lbw_attention_fwd_fp8kv", "lbw_attention_fwd_noalloc", "lbw_attn_merge", "lbw_qk_norm_rope",
+    "lbw_attention_fwd_fp8kv", "lbw_attention_fwd_noalloc", "lbw_attn_merge",
+    "lbw_attn_merge_partials", "lbw_qk_norm_rope",
     "lbw_kv_quant_fp8",
     "lbw_last_error", "lbw_abi_version",
 )
@@ -108,6 +109,9 @@ def _declare(lib):
     lib.lbw_attn_merge.argtypes = [i32, P(vp), P(vp), P(vp), i32, i32, i32, i32, vp, i64, i64,
                                    i64, vp]
     lib.lbw_attn_merge.restype = ctypes.c_int
+    lib.lbw_attn_merge_partials.argtypes = [i32, P(vp), P(vp), P(vp), i32, i32, i32, i32, vp, vp,
+                                            vp, vp]
+    lib.lbw_attn_merge_partials.restype = ctypes.c_int
     lib.lbw_qk_norm_rope.argtypes = [P(QkNormRopeParams), vp]
     lib.lbw_qk_norm_rope.restype = ctypes.c_int
     lib.lbw_kv_quant_fp8.argtypes = [vp, i32, i64, i32, i32, i64, i64, i64, vp, vp, i32, vp]

@@ -23,7 +23,8 @@ import torch
 from . import _lib
 
 __all__ = ["attention", "flash_attention", "exact_attention", "exact_attention_chunks",
-           "cross_attention", "attention_partial", "attention_merge", "attention_chain",
+           "cross_attention", "attention_partial", "attention_merge", "attention_merge_partials",
+           "attention_chain",
            "attention_segments", "window_from_mask", "PRESCALED_SOFTMAX_SCALE",
            "prescaled_q_scale"]
 
@@ -257,6 +258,15 @@ def attention_merge(parts, out: torch.Tensor | None = None) -> torch.Tensor:
     ops = _lib.ops()
     if not 1 <= len(parts) <= 16:
         raise ValueError("1..16 partials")
+    _check_parts(parts)
+    os_, ms, ls = [p[0] for p in parts], [p[1] for p in parts], [p[2] for p in parts]
+    if out is None:
+        return ops.attention_merge(os_, ms, ls)
+    ops.attention_merge_out(os_, ms, ls, out)
+    return out
+
+
+def _check_parts(parts):
     po0 = parts[0][0]
     B, H, Lq, D = po0.shape
     for o, m, l in parts:
@@ -266,11 +276,17 @@ def attention_merge(parts, out: torch.Tensor | None = None) -> torch.Tensor:
             raise ValueError("partials must be contiguous")
         if o.dtype != torch.float32 or m.dtype != torch.float32 or l.dtype != torch.float32:
             raise ValueError("partials must be float32")
-    os_, ms, ls = [p[0] for p in parts], [p[1] for p in parts], [p[2] for p in parts]
-    if out is None:
-        return ops.attention_merge(os_, ms, ls)
-    ops.attention_merge_out(os_, ms, ls, out)
-    return out
+
+
+def attention_merge_partials(parts):
+    """The log-sum-exp merge of partials ``(O, m, l)`` into one partial triple (O relative to
+    the merged row max M, m = M, l the merged row sum): the running state of cte_call's chain
+    (attention.py:654-694). ``attention_merge`` of the result normalises it."""
+    if not 1 <= len(parts) <= 16:
+        raise ValueError("1..16 partials")
+    _check_parts(parts)
+    return _lib.ops().attention_merge_partials([p[0] for p in parts], [p[1] for p in parts],
+                                               [p[2] for p in parts])
 
 
 def attention_chain(q, segments, chain=None, normalize=False, *, kv_lo=None, kv_hi=None,
@@ -280,18 +296,19 @@ def attention_chain(q, segments, chain=None, normalize=False, *, kv_lo=None, kv_
     ``normalize=True`` returns the attention over the union of every call's keys, bf16
     ``[B, Lq, N, D]``. Without it the call returns the new chain state.
 
-    The state is the tuple of the calls' partials ``(O, m, l)`` (attention_partial), combined
-    exactly by one log-sum-exp merge at the normalizing call, where the reference carries one
-    running (O, -max, sum) triple; the result is the same softmax. At most 16 calls."""
-    parts = tuple(chain) if chain is not None else ()
+    The state is one running triple ``(O, m, l)`` as the reference's (O, -max, sum): each call's
+    partials (attention_partial) are merged into it by ``attention_merge_partials``, so its size
+    does not grow with the number of calls; the normalizing call divides it out."""
+    state = chain
     if segments:
-        parts = parts + (attention_partial(q, segments, kv_lo=kv_lo, kv_hi=kv_hi,
-                                           softmax_scale=softmax_scale),)
+        part = attention_partial(q, segments, kv_lo=kv_lo, kv_hi=kv_hi,
+                                 softmax_scale=softmax_scale)
+        state = part if state is None else attention_merge_partials([state, part])
     if not normalize:
-        return parts
-    if not parts:
+        return state
+    if state is None:
         raise ValueError("a chain needs at least one call with keys")
-    return attention_merge(parts, out=out)
+    return attention_merge([state], out=out)
 
 
 def default_scale(head_dim: int) -> float:

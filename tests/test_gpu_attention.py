@@ -395,3 +395,45 @@ def test_split_pieces_merged_in_kernel(lib, splits):
     for r in runs[1:]:
         assert torch.equal(r, runs[0])
     assert torch.equal(o32.to(torch.bfloat16), runs[0])
+
+
+def test_chain_state_is_one_running_triple(lib):
+    """The chain state is one (O, m, l) triple merged call by call (the reference's running
+    (O, -max, sum)): 20 calls -- more than one merge launch takes partials -- over 20 key
+    sets, one of them empty, equal attention over their union; the state after the calls is
+    the union's partials: m the row max of all scores, l and O relative to it."""
+    from lbw_amd import attention_chain
+    lens = [64 * (i % 5) + 17 * i for i in range(20)]
+    q, ks, vs = _case(1, 150, 2, lens, seed=77, gain=False)
+    qd = q.to(DEV)
+    state = None
+    for k, v in zip(ks, vs):
+        state = attention_chain(qd, [(k.to(DEV), v.to(DEV))] if k.shape[1] else [], state)
+        assert state is None or len(state) == 3
+    out = attention_chain(qd, [], state, normalize=True)
+    torch.cuda.synchronize()
+    kk, vv = torch.cat(ks, 1), torch.cat(vs, 1)
+    assert_parity(out, O.attention_ref(q, kk, vv), "20-call chain")
+    _, (ro, rm, rl) = O.attention_ref(q, kk, vv, return_partials=True)
+    po, pm, pl = state
+    assert torch.allclose(pm.cpu(), rm, rtol=1e-5, atol=1e-4)
+    assert torch.allclose(pl.cpu(), rl, rtol=5e-3, atol=1e-3)
+    # O is relative to the row max (sums of up to hundreds of bf16 p): held as the normalised
+    # rows and by its relative L1 error
+    po, pl = po.cpu(), pl.cpu()
+    assert torch.allclose(po / pl[..., None], ro / rl[..., None], atol=1e-2)
+    assert float((po - ro).abs().mean() / ro.abs().mean()) <= 4e-3
+
+
+def test_merge_partials_of_empty_rows(lib):
+    """Rows with no keys in any partial (m = -inf, l = 0) merge to m = -inf, l = 0, O = 0, and
+    normalise to 0, as SDPA's fully masked rows."""
+    from lbw_amd import attention_merge, attention_merge_partials, attention_partial
+    q, ks, vs = _case(1, 40, 2, [300], seed=3)
+    segs = [(ks[0].to(DEV), vs[0].to(DEV))]
+    a = attention_partial(q.to(DEV), segs, kv_lo=100, kv_hi=100)
+    b = attention_partial(q.to(DEV), segs, kv_lo=0, kv_hi=0)
+    po, pm, pl = attention_merge_partials([a, b])
+    torch.cuda.synchronize()
+    assert torch.all(torch.isneginf(pm)) and torch.all(pl == 0) and torch.all(po == 0)
+    assert torch.all(attention_merge([(po, pm, pl)]) == 0)
