@@ -52,7 +52,13 @@ enum {
 
 /* One contiguous piece of the KV sequence, tokens-major [B, len, H, D]. The attention sees
  * the concatenation of the segments in order (e.g. the cached frames then the current
- * chunk, or the chunked cache's (leading..., destination) buffers), without a copy. */
+ * chunk, or the chunked cache's (leading..., destination) buffers), without a copy.
+ * K may instead be d-major, the reference's N-major K cache [H, D, L] (and its pre-transposed
+ * cross cache): k_stride_d > 0 puts element (b, t, h, d) of K at b * k_stride_b + h * k_stride_h
+ * + d * k_stride_d + t, token stride 1 (k_stride_l must then be 1); bf16 entry points only,
+ * every segment of the call d-major, len and the strides multiples of 8
+ * (wan/modules/chunked_kv_cache.py:118-148, wan/modules/attention.py:494-499, 557-579). V is
+ * token-major per head in both of those layouts ([H, L, D] is a strided [B, L, H, D]). */
 typedef struct lbw_kv_segment {
   const void* k;        /* bf16, or e4m3fn codes (uint8) for the fp8 entry point */
   const void* v;
@@ -61,6 +67,7 @@ typedef struct lbw_kv_segment {
   int64_t v_stride_b, v_stride_l, v_stride_h;
   const float* k_scale; /* fp8 only: [B, H, ceil(len / 64)] fp32, contiguous */
   const float* v_scale;
+  int64_t k_stride_d;   /* 0: K token-major (head dim contiguous); > 0: K d-major (above) */
 } lbw_kv_segment;
 
 typedef struct lbw_attn_params {

@@ -19,6 +19,7 @@ struct SegDesc {
   const float* ks;    // fp8 scales [B, H, nblk]
   const float* vs;
   int64_t nblk;       // scale blocks per (b, h)
+  int64_t ksd;        // d-major K: the d stride (token stride 1); 0: K token-major
 };
 
 struct AttnKernelArgs {
@@ -50,6 +51,7 @@ struct AttnKernelArgs {
   float mult_raw;     // ln(multiplicity) / scale: added to those keys' raw scores
   int track_max;      // partials must carry the true row max (cte_partial contract); otherwise
                       // any exponent reference consistent with O and l will do
+  int k_dmajor;       // every segment's K is d-major (SegDesc::ksd)
 };
 
 struct MergeKernelArgs {

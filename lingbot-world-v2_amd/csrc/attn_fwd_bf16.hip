@@ -249,10 +249,18 @@ __device__ void merge_unit(const AttnKernelArgs& a, int b, int h, int qt, int ro
 // SEGN = 1 or 2: that many KV segments (a flat cache's window; a cache and the current chunk),
 // no multiplicity bias and, for two, the same row strides: the tile copies are addressed by the
 // tile index (issue1, issue_raw1, issue_k81) instead of walked by the general cursor (SEGN 0).
-template <bool FP8, bool TRACK, bool FOLD, int SEGN>
+// KDM: K is d-major (the reference's N-major K cache [H, D, L], token stride 1). A K tile is then
+// held in LDS as its two 32-key halves, each [128 d-rows][32 keys] (64-byte rows), copied 16 bytes
+// (8 keys of one d) per lane; the QK operand of a key is gathered from a d-row pair of reads by
+// the LDS transpose read (as V^T is from V rows), which gives lane (key, hl) the d values
+// 16s + 4hl + {0..3, 8..11} of d-slice s, and the query operand is loaded in that same d order.
+// Every read pattern of a 32-lane pass covers the 64 banks once (four 64-byte rows), so the halves
+// need no swizzle.
+template <bool FP8, bool TRACK, bool FOLD, int SEGN, bool KDM = false>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   static_assert(!FOLD || (!FP8 && !TRACK), "the folded softmax is the plain bf16 form");
+  static_assert(!KDM || (!FP8 && SEGN == 0), "d-major K: bf16, general tile cursor");
   constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
@@ -299,7 +307,16 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     for (int s = 0; s < 8; ++s) {
       const int d0 = FP8 ? 32 * (s >> 1) + 16 * hl + 8 * (s & 1) : 16 * s + 8 * hl;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (q < a.Lq) v = *reinterpret_cast<const u32x4*>(qp + d0);
+      if constexpr (KDM) {
+        // d = 16s + 4hl + {0..3, 8..11}: the order of the d-major K operand (see the kernel note)
+        if (q < a.Lq) {
+          const u32x2 x0 = *reinterpret_cast<const u32x2*>(qp + 16 * s + 4 * hl);
+          const u32x2 x1 = *reinterpret_cast<const u32x2*>(qp + 16 * s + 4 * hl + 8);
+          v = u32x4{x0[0], x0[1], x1[0], x1[1]};
+        }
+      } else {
+        if (q < a.Lq) v = *reinterpret_cast<const u32x4*>(qp + d0);
+      }
       qf[s] = v;
     }
     // (waited for below, together with the first K/V tiles: one round trip, not two)
@@ -334,6 +351,16 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     dma_row[i] = 4 * (NDMA * wave + i) + (lane >> 4);
     dma_col[i] = ((lane & 15) ^ swz(dma_row[i])) * 16;  // byte offset of the logical chunk
   }
+  // d-major K: block j = NDMA * wave + i is half j / 8, d-rows 16 (j % 8) + lane / 4 of it, and
+  // the lane's 8 keys 32 (j / 8) + 8 (lane % 4) .. +7 of the tile (LDS byte 1024 j + 16 lane, as
+  // for token-major rows)
+  int kdm_row[NDMA], kdm_key[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int j = NDMA * wave + i;
+    kdm_row[i] = 16 * (j & 7) + (lane >> 2);
+    kdm_key[i] = 32 * (j >> 3) + 8 * (lane & 3);
+  }
   // LDS byte addresses of this lane's fragments in stage 0.
   // K fragment (sub-block rows 0..31) for d-slice s: row l32, logical chunk 2s + hl. fp8: the
   // x64 operand of d-half m is the two 16-byte reads koff[2m] (bytes 0-15, chunk 4m + hl) and
@@ -344,8 +371,19 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   for (int s = 0; s < 8; ++s) {
     if constexpr (FP8)
       koff[s] = s < 4 ? opaque(lds0 + l32 * ROWB8 + (((2 * s + hl) ^ swz8(l32)) << 4)) : 0;
+    else if constexpr (KDM)
+      koff[s] = 0;
     else
       koff[s] = opaque(lds0 + l32 * ROWB + (((2 * s + hl) ^ swz(l32)) << 4));
+  }
+  // d-major K transpose reads (half 0, d-slice 0, first read): the 16-lane group (lane / 16)
+  // takes keys 16 (group % 2) .. +15 of the half and d-rows 4hl .. +3; source lane s16 points at
+  // d-row 4hl + s16 / 4, keys 16 (group % 2) + 4 (s16 % 4) .. +3 (byte 8 (s16 % 2) of its 16-byte
+  // chunk). d-slice s adds 16 rows (1 KB), the second read 8 rows (512 B), half 1 adds 8 KB.
+  int kdm_off = 0;
+  if constexpr (KDM) {
+    const int s16 = lane & 15, g = (lane >> 4) & 1;
+    kdm_off = opaque(lds0 + (4 * hl + (s16 >> 2)) * 64 + (2 * g + ((s16 & 3) >> 1)) * 16 + 8 * (s16 & 1));
   }
   // V transpose reads (sub-block rows 0..31, k-step m = 0) for d-block db and key
   // half j: source row 4hl + 8j + s/4, columns 32db + 16g + 4(s%4) .. +3 (s = lane % 16,
@@ -388,7 +426,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   auto seg_offsets = [&]() {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
-      lane_k[i] = (uint32_t)dma_row[i] * cs.ks + dma_col[i];
+      lane_k[i] = KDM ? (uint32_t)kdm_row[i] * cs.ks + 2 * kdm_key[i]
+                      : (uint32_t)dma_row[i] * cs.ks + dma_col[i];
       lane_v[i] = (uint32_t)dma_row[i] * cs.vs + dma_col[i];
     }
   };
@@ -410,7 +449,15 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       for (int i = 0; i < NDMA; ++i) {
         int r = dma_row[i];
         r = r < tvlo ? tvlo : (r > rhi ? rhi : r);
-        dma16(cs.kt, (uint32_t)r * cs.ks + dma_col[i], kdst + 1024 * i);
+        if constexpr (KDM) {
+          // a lane's 8 keys lie in the segment when its first does (len is a multiple of 8);
+          // groups wholly outside the valid rows copy a valid group instead
+          int kk = kdm_key[i];
+          kk = kk < (tvlo & ~7) ? (tvlo & ~7) : (kk > (rhi & ~7) ? (rhi & ~7) : kk);
+          dma16(cs.kt, (uint32_t)kdm_row[i] * cs.ks + 2 * kk, kdst + 1024 * i);
+        } else {
+          dma16(cs.kt, (uint32_t)r * cs.ks + dma_col[i], kdst + 1024 * i);
+        }
         dma16(cs.vt, (uint32_t)r * cs.vs + dma_col[i], vdst + 1024 * i);
       }
     }
@@ -661,6 +708,10 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           k8f[i][j] = (int)x0[j];
           k8f[i][j + 4] = (int)x1[j];
         }
+      } else if constexpr (KDM) {
+        const u32x2 x0 = lds_read_tr16(kdm_off + KO + 1024 * i);
+        const u32x2 x1 = lds_read_tr16(kdm_off + KO + 1024 * i + 512);
+        kf[i % KR] = u32x4{x0[0], x0[1], x1[0], x1[1]};
       } else {
         kf[i % KR] = lds_read_b128(koff[i] + KO);
       }
@@ -686,7 +737,15 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         load_k(std::integral_constant<int, HALF8_B>{}, 0);
       } else {
 #pragma unroll
-        for (int s = 0; s < 8; ++s) sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
+        for (int s = 0; s < 8; ++s) {
+          if constexpr (KDM) {
+            const u32x2 x0 = lds_read_tr16(kdm_off + 1024 * s);
+            const u32x2 x1 = lds_read_tr16(kdm_off + 1024 * s + 512);
+            sA = mfma32x32x16(u32x4{x0[0], x0[1], x1[0], x1[1]}, qf[s], sA);
+          } else {
+            sA = mfma32x32x16(lds_read_b128(koff[s]), qf[s], sA);
+          }
+        }
 #pragma unroll
         for (int i = 0; i < K_AHEAD; ++i) load_k(std::integral_constant<int, HALF_B>{}, i);
       }
@@ -1140,9 +1199,9 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-template <bool FP8, bool TRACK, bool FOLD = false, int SEGN = 0>
+template <bool FP8, bool TRACK, bool FOLD = false, int SEGN = 0, bool KDM = false>
 static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN>,
+  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN, KDM>,
                                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t U = (uint32_t)a.n_qtiles * a.H * a.B;
@@ -1157,8 +1216,8 @@ static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(attn_queue_reset_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64),
                        dim3(256), 0, stream, a.queue, n);
   }
-  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN>), dim3(nwg), dim3(NWAVE * 64), LDS_B,
-                     stream, a);
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN, KDM>), dim3(nwg), dim3(NWAVE * 64),
+                     LDS_B, stream, a);
   return hipGetLastError();
 }
 
@@ -1171,6 +1230,11 @@ static int index_segments(const AttnKernelArgs& a) {
 }
 
 hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
+  if (a.k_dmajor) {  // d-major K: the general cursor
+    if (a.track_max) return launch<false, true, false, 0, true>(a, stream);
+    if (a.scale_log2 == 1.0f) return launch<false, false, true, 0, true>(a, stream);
+    return launch<false, false, false, 0, true>(a, stream);
+  }
   if (a.track_max) return launch<false, true>(a, stream);
   // a pre-scaled q (scale * log2(e) exactly 1 in fp32) takes the folded softmax
   const int segn = index_segments(a);

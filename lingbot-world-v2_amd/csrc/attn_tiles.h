@@ -182,9 +182,11 @@ __device__ __forceinline__ void cursor_enter(const AttnKernelArgs& a, int i, int
   c.lb = (int)lb;
   c.lt = lt;
   c.lt_end = (int)((lb + BN - 1) / BN);
-  c.ks = (uint32_t)(s.ksl * ESZ);
+  // (d-major K: ks is the byte stride of its d-rows and a tile starts BN tokens further along
+  // each row)
+  c.ks = (uint32_t)((s.ksd != 0 ? s.ksd : s.ksl) * ESZ);
   c.vs = (uint32_t)(s.vsl * ESZ);
-  c.kstep = (uint32_t)(s.ksl * ESZ * BN);
+  c.kstep = (uint32_t)((s.ksd != 0 ? 1 : s.ksl) * ESZ * BN);
   c.vstep = (uint32_t)(s.vsl * ESZ * BN);
   c.kt = reinterpret_cast<const unsigned char*>(s.k) + (s.ksb * b + s.ksh * h) * ESZ +
          (int64_t)lt * c.kstep;

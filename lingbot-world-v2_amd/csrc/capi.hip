@@ -168,6 +168,26 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   a.o16 = aligned16(p->out) && mult8(p->o_stride_b) && mult8(p->o_stride_l) && mult8(p->o_stride_h);
   a.o32 = o32 ? 1 : 0;
   a.nseg = p->n_segments;
+  // d-major K: every segment or none, bf16 only
+  a.k_dmajor = p->seg[0].k_stride_d != 0;
+  for (int i = 0; i < p->n_segments; ++i) {
+    const lbw_kv_segment& s = p->seg[i];
+    if ((s.k_stride_d != 0) != (a.k_dmajor != 0))
+      return fail(LBW_ERR_INVALID, "segment %d: every segment's K must be d-major, or none", i);
+    if (s.k_stride_d == 0) continue;
+    if (fp8) return fail(LBW_ERR_UNSUPPORTED, "d-major K: bf16 segments only");
+    if (s.k_stride_d < 0 || s.k_stride_l != 1)
+      return fail(LBW_ERR_INVALID, "segment %d: d-major K needs k_stride_l = 1 and k_stride_d > 0", i);
+    if ((s.len & 7) || (s.k_stride_d & 7) || (s.k_stride_b & 7) || (s.k_stride_h & 7))
+      return fail(LBW_ERR_INVALID,
+                  "segment %d: d-major K needs len and its strides multiples of 8 elements", i);
+    if (s.len > 0 && s.k_stride_d < s.len)
+      return fail(LBW_ERR_INVALID, "segment %d: d-major K d stride %lld below len %lld", i,
+                  (long long)s.k_stride_d, (long long)s.len);
+    // a tile's 128 d-rows are addressed with 32-bit offsets from its first
+    if (s.k_stride_d * 2 * 128 >= (int64_t(1) << 32))
+      return fail(LBW_ERR_UNSUPPORTED, "segment %d: d-major K d stride too large", i);
+  }
   int64_t start = 0;
   for (int i = 0; i < p->n_segments; ++i) {
     const lbw_kv_segment& s = p->seg[i];
@@ -179,7 +199,7 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
       if (s.k == nullptr || s.v == nullptr || !aligned16(s.k) || !aligned16(s.v))
         return fail(LBW_ERR_INVALID, "segment %d: k/v must be 16-byte aligned device pointers", i);
       const int64_t el = fp8 ? 16 : 8;  // 16-byte granules in elements
-      if ((s.k_stride_b % el) || (s.k_stride_l % el) || (s.k_stride_h % el) ||
+      if ((s.k_stride_b % el) || (s.k_stride_l % el && s.k_stride_d == 0) || (s.k_stride_h % el) ||
           (s.v_stride_b % el) || (s.v_stride_l % el) || (s.v_stride_h % el))
         return fail(LBW_ERR_INVALID, "segment %d: strides must be multiples of %lld elements", i,
                     (long long)el);
@@ -199,6 +219,7 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
     d.vsb = s.v_stride_b; d.vsl = s.v_stride_l; d.vsh = s.v_stride_h;
     d.ks = s.k_scale; d.vs = s.v_scale;
     d.nblk = (s.len + LBW_FP8_BLOCK - 1) / LBW_FP8_BLOCK;
+    d.ksd = s.k_stride_d;
     start += s.len;
   }
   a.total = start;
@@ -259,6 +280,8 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
   // context the host knows to be longer goes to the chunk kernel as a single pass, which
   // streams it faster than the cross kernel's chunk reloads.
   if (cross && a.k_lens == nullptr && a.hi - a.lo > cross_attn_max_keys_resident()) cross = false;
+  // (the cross kernel reads K token-major: a d-major context runs the chunk kernel, one pass)
+  if (cross && a.k_dmajor) cross = false;
   if (cross) {
     // one segment, single pass: the persistent cross-attention kernel; its chunk loads address
     // up to 320 rows with 32-bit offsets from the chunk's first row

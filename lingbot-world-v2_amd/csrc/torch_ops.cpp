@@ -32,10 +32,12 @@ void* stream_of(const at::Tensor& t) {
   return c10::hip::getCurrentHIPStream(t.get_device()).stream();
 }
 
-void check_bf16_4d(const char* name, const at::Tensor& t) {
+void check_bf16_4d(const char* name, const at::Tensor& t, bool dmajor_ok = false) {
   TORCH_CHECK(t.is_cuda(), name, " must be a GPU tensor");
   TORCH_CHECK(t.dim() == 4, name, " must be [B, L, N, D]");
-  TORCH_CHECK(t.stride(3) == 1, name, " needs a contiguous head dim");
+  TORCH_CHECK(t.stride(3) == 1 || (dmajor_ok && t.stride(1) == 1), name,
+              dmajor_ok ? " needs a contiguous head dim, or token stride 1 (d-major)"
+                        : " needs a contiguous head dim");
 }
 
 // A device window bound: a one-element integer tensor on q's device (the flat cache's attn_lo /
@@ -86,7 +88,7 @@ lbw_attn_params base_params(const at::Tensor& q, at::TensorList k, at::TensorLis
   for (size_t i = 0; i < k.size(); ++i) {
     const at::Tensor& kt = k[i];
     const at::Tensor& vt = v[i];
-    check_bf16_4d("k", kt);
+    check_bf16_4d("k", kt, kv_type == at::kBFloat16);  // (a d-major K view: token stride 1)
     check_bf16_4d("v", vt);
     TORCH_CHECK(kt.device() == q.device() && vt.device() == q.device(),
                 "k/v must be on q's device");
@@ -98,6 +100,7 @@ lbw_attn_params base_params(const at::Tensor& q, at::TensorList k, at::TensorLis
     s.v = vt.data_ptr();
     s.len = kt.size(1);
     s.k_stride_b = kt.stride(0); s.k_stride_l = kt.stride(1); s.k_stride_h = kt.stride(2);
+    s.k_stride_d = kt.stride(3) == 1 ? 0 : kt.stride(3);
     s.v_stride_b = vt.stride(0); s.v_stride_l = vt.stride(1); s.v_stride_h = vt.stride(2);
   }
   p.kv_lo = kv_lo;

@@ -32,6 +32,7 @@ class KvSegment(ctypes.Structure):
         ("k_stride_b", ctypes.c_int64), ("k_stride_l", ctypes.c_int64), ("k_stride_h", ctypes.c_int64),
         ("v_stride_b", ctypes.c_int64), ("v_stride_l", ctypes.c_int64), ("v_stride_h", ctypes.c_int64),
         ("k_scale", ctypes.c_void_p), ("v_scale", ctypes.c_void_p),
+        ("k_stride_d", ctypes.c_int64),
     ]
 
 
@@ -191,6 +192,8 @@ def attn_params(q, out, segments, kv_lo=None, kv_hi=None, k_lens=None, softmax_s
         seg = p.seg[i]
         seg.k, seg.v, seg.len = k.data_ptr(), v.data_ptr(), k.shape[1]
         seg.k_stride_b, seg.k_stride_l, seg.k_stride_h = k.stride(0), k.stride(1), k.stride(2)
+        if k.stride(3) != 1:   # d-major K: [B, L, N, D] view with token stride 1
+            seg.k_stride_d = k.stride(3)
         seg.v_stride_b, seg.v_stride_l, seg.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
         if len(sg) > 2:
             seg.k_scale, seg.v_scale = sg[2].data_ptr(), sg[3].data_ptr()

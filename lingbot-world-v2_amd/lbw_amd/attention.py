@@ -44,6 +44,15 @@ def _as_bf16(t: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def _as_bf16_k(t: torch.Tensor) -> torch.Tensor:
+    """A K segment: token-major ``[B, L, N, D]`` with a contiguous head dim, or a d-major view
+    of the reference's N-major K cache (``k_ndl.permute(2, 0, 1)[None]`` of an ``[N, D, L]``
+    buffer: token stride 1), which the kernel reads as it lies."""
+    if t.dtype == torch.bfloat16 and t.dim() == 4 and t.stride(-1) != 1 and t.stride(1) == 1:
+        return t
+    return _as_bf16(t)
+
+
 def _check_4d(name, t, device):
     if t.dim() != 4:
         raise ValueError(f"{name} must be [B, L, N, D], got shape {tuple(t.shape)}")
@@ -79,7 +88,8 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     """softmax(scale Q K^T) V over the windowed concatenation of KV ``segments``.
 
     q ``[B, Lq, N, 128]``; each segment is ``(k, v)`` with k/v ``[B, L_i, N, 128]`` (strided
-    views are fine as long as the head dim is contiguous); the window ``[kv_lo, kv_hi)``
+    views are fine as long as the head dim is contiguous; K may instead be a d-major view, token
+    stride 1, of the reference's N-major ``[N, D, L]`` K cache -- every segment's or none); the window ``[kv_lo, kv_hi)``
     indexes the concatenation (ints, or one-element integer tensors on q's device that the
     kernel reads there, so the call needs no host sync). ``k_lens`` (int32 ``[B]`` on the device) limits each batch's
     keys. With ``cross``, a single short segment; ``n_distinct`` (cross only) declares keys
@@ -127,7 +137,7 @@ def _segments(segments, device):
     for k, v in segments:
         _check_4d("k", k, device)
         _check_4d("v", v, device)
-        ks.append(_as_bf16(k))
+        ks.append(_as_bf16_k(k))
         vs.append(_as_bf16(v))
     return ks, vs
 
