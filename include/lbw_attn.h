@@ -102,6 +102,12 @@ typedef struct lbw_attn_params {
    * bounds alone. The split plan assumes the host window; cross-attention takes neither. */
   const int64_t* kv_lo_dev;
   const int64_t* kv_hi_dev;
+  /* Optional per-key additive score bias, fp32 [total keys of the segments] on the device,
+   * natural-log units added to the scaled scores and shared by every batch and head:
+   * softmax(scale q k^T + bias) v, as cross_attention_dedup's bias (attention.py:532-554). NULL
+   * = none. Not with partials outputs, the fp8 entry point or n_distinct (the dedup entry's own
+   * bias). Calls with a bias run a kernel instance of their own. */
+  const float* key_bias;
 } lbw_attn_params;
 #define LBW_OUT_BF16 0
 #define LBW_OUT_FP32 1

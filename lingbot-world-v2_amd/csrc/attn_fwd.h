@@ -52,6 +52,8 @@ struct AttnKernelArgs {
   int track_max;      // partials must carry the true row max (cte_partial contract); otherwise
                       // any exponent reference consistent with O and l will do
   int k_dmajor;       // every segment's K is d-major (SegDesc::ksd)
+  const float* key_bias;  // per-key score bias over the concatenated keys (natural log), or null
+  float inv_scale;        // 1 / scale: the bias in raw-score units
 };
 
 struct MergeKernelArgs {

@@ -52,6 +52,7 @@ constexpr int NSTAGE = 3;               // tiles resident or in flight
 constexpr int V_BASE = 65536;           // V tiles start here; K tiles at NSTAGE * 16 KB below
 constexpr int LDS_B = V_BASE + NSTAGE * TILE_B;
 constexpr int NDMA = TILE_B / (NWAVE * 64 * 16);  // 16-byte DMA blocks per lane per K/V tile
+constexpr int BIAS_BASE = NSTAGE * TILE_B;        // key-bias stages (256 B each), below V_BASE
 // MFMA pairs ahead that a step's K (QK chain) and V (PV) fragments are read from LDS
 constexpr int K_AHEAD = 2, V_AHEAD = 2;
 static_assert(NSTAGE * TILE_B <= V_BASE, "K tiles must fit below the V tiles");
@@ -256,11 +257,15 @@ __device__ void merge_unit(const AttnKernelArgs& a, int b, int h, int qt, int ro
 // 16s + 4hl + {0..3, 8..11} of d-slice s, and the query operand is loaded in that same d order.
 // Every read pattern of a 32-lane pass covers the 64 banks once (four 64-byte rows), so the halves
 // need no swizzle.
-template <bool FP8, bool TRACK, bool FOLD, int SEGN, bool KDM = false>
+// BIAS: a per-key additive score bias (natural log, shared by batch and heads): each tile's 64
+// bias values are copied with the tile into LDS by wave 0, and every step adds them to its scores
+// (in raw-score units: bias / scale) before the softmax.
+template <bool FP8, bool TRACK, bool FOLD, int SEGN, bool KDM = false, bool BIAS = false>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
   static_assert(!FOLD || (!FP8 && !TRACK), "the folded softmax is the plain bf16 form");
   static_assert(!KDM || (!FP8 && SEGN == 0), "d-major K: bf16, general tile cursor");
+  static_assert(!BIAS || (!FP8 && !TRACK && !FOLD && SEGN == 0), "key bias: plain bf16 form");
   constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
   extern __shared__ __attribute__((aligned(1024))) unsigned char lds[];
   const int lane = threadIdx.x & 63;
@@ -459,6 +464,14 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           dma16(cs.kt, (uint32_t)r * cs.ks + dma_col[i], kdst + 1024 * i);
         }
         dma16(cs.vt, (uint32_t)r * cs.vs + dma_col[i], vdst + 1024 * i);
+      }
+    }
+    if constexpr (BIAS) {
+      // the tile's 64 key biases (clamped to the last key past the end: those keys are masked)
+      if (wave == 0) {
+        int64_t key = a.seg[cs.seg].start + (int64_t)cs.lt * BN + lane;
+        key = key < a.total - 1 ? key : a.total - 1;
+        dma4((uint64_t)(uintptr_t)(a.key_bias + key), (uint32_t)sreg(lds0) + BIAS_BASE + stage * 256);
       }
     }
     if (cursor_next<ESZ>(a, lo, hi, b, h, mult, cs) && cs.seg < a.nseg) seg_offsets();
@@ -777,6 +790,20 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
       if constexpr (TRACK) {
         if (pend) scale_acc(oacc, alpha_p);
+      }
+      if constexpr (BIAS) {
+        // this lane's keys 32 kb + 8 g + 4 hl .. +3 (registers 4g .. 4g+3) of the tile being
+        // softmaxed (stage KS for the first half's step, the stage before SN for the second's)
+        constexpr int KS = decltype(koff_c)::value / (FP8 ? TILE8_B : TILE_B);
+        const int st = kb == 0 ? KS : (KS + NSTAGE - 1) % NSTAGE;
+        const float inv_scale = a.inv_scale;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const u32x4 bv = lds_read_b128(lds0 + BIAS_BASE + 256 * st + 128 * kb + 32 * g + 16 * hl);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            s_in[4 * g + e] = __builtin_fmaf(__uint_as_float(bv[e]), inv_scale, s_in[4 * g + e]);
+        }
       }
       const int vlo = vrow & 0xff, vhi = (vrow >> 8) & 0xff, mrow = vrow >> 16;
       if (vrow != ROWS_FULL && (vlo > 32 * kb || vhi < 32 * kb + 32 || mrow < 32 * kb + 32))
@@ -1199,10 +1226,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 
 }  // namespace
 
-template <bool FP8, bool TRACK, bool FOLD = false, int SEGN = 0, bool KDM = false>
+template <bool FP8, bool TRACK, bool FOLD = false, int SEGN = 0, bool KDM = false, bool BIAS = false>
 static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
-  static hipError_t attr = hipFuncSetAttribute((const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN, KDM>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
+  static hipError_t attr = hipFuncSetAttribute(
+      (const void*)attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN, KDM, BIAS>,
+      hipFuncAttributeMaxDynamicSharedMemorySize, LDS_B);
   if (attr != hipSuccess) return attr;
   const uint32_t U = (uint32_t)a.n_qtiles * a.H * a.B;
   const uint32_t per_xcd = a.splits * ((U + 7u) / 8u);  // items of the largest XCD share
@@ -1216,8 +1244,8 @@ static hipError_t launch(const AttnKernelArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(attn_queue_reset_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64),
                        dim3(256), 0, stream, a.queue, n);
   }
-  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN, KDM>), dim3(nwg), dim3(NWAVE * 64),
-                     LDS_B, stream, a);
+  hipLaunchKernelGGL((attn_fwd_bf16_kernel<FP8, TRACK, FOLD, SEGN, KDM, BIAS>), dim3(nwg),
+                     dim3(NWAVE * 64), LDS_B, stream, a);
   return hipGetLastError();
 }
 
@@ -1230,6 +1258,10 @@ static int index_segments(const AttnKernelArgs& a) {
 }
 
 hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
+  if (a.key_bias != nullptr) {  // a per-key bias: the plain form (any scale), general cursor
+    return a.k_dmajor ? launch<false, false, false, 0, true, true>(a, stream)
+                      : launch<false, false, false, 0, false, true>(a, stream);
+  }
   if (a.k_dmajor) {  // d-major K: the general cursor
     if (a.track_max) return launch<false, true, false, 0, true>(a, stream);
     if (a.scale_log2 == 1.0f) return launch<false, false, true, 0, true>(a, stream);

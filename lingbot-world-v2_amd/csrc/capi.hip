@@ -228,10 +228,14 @@ int make_plan(const lbw_attn_params* p, bool fp8, Plan* plan) {
   if (a.hi < a.lo) a.hi = a.lo;
   a.lo_dev = p->kv_lo_dev;
   a.hi_dev = p->kv_hi_dev;
+  a.key_bias = p->key_bias;
+  if (a.key_bias != nullptr && (fp8 || partials))
+    return fail(LBW_ERR_UNSUPPORTED, "key_bias: bf16 normalised outputs only (no fp8, no partials)");
   a.k_lens = p->k_lens;
   const float scale = p->softmax_scale > 0.0f ? p->softmax_scale : 1.0f / sqrtf((float)p->head_dim);
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.inv_scale = 1.0f / scale;
   a.B = p->batch; a.H = p->heads; a.Lq = p->lq;
   const int bm = attn_block_m(), bn = attn_block_n();
   a.n_qtiles = (p->lq + bm - 1) / bm;
@@ -280,8 +284,9 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
   // context the host knows to be longer goes to the chunk kernel as a single pass, which
   // streams it faster than the cross kernel's chunk reloads.
   if (cross && a.k_lens == nullptr && a.hi - a.lo > cross_attn_max_keys_resident()) cross = false;
-  // (the cross kernel reads K token-major: a d-major context runs the chunk kernel, one pass)
-  if (cross && a.k_dmajor) cross = false;
+  // (the cross kernel reads K token-major and takes no general bias: such a context runs the
+  // chunk kernel, one pass)
+  if (cross && (a.k_dmajor || a.key_bias != nullptr)) cross = false;
   if (cross) {
     // one segment, single pass: the persistent cross-attention kernel; its chunk loads address
     // up to 320 rows with 32-bit offsets from the chunk's first row
@@ -423,6 +428,8 @@ int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, 
   if (p->k_lens != nullptr || p->kv_lo != 0 || p->kv_hi >= 0 || p->kv_lo_dev != nullptr ||
       p->kv_hi_dev != nullptr)
     return fail(LBW_ERR_INVALID, "dedup attends the whole context: no k_lens or window");
+  if (p->key_bias != nullptr)
+    return fail(LBW_ERR_INVALID, "dedup carries its own bias: no key_bias");
   if (p->num_splits > 1) return fail(LBW_ERR_INVALID, "cross-attention is single pass");
   if (p->part_o != nullptr || p->part_m != nullptr || p->part_l != nullptr)
     return fail(LBW_ERR_INVALID, "cross-attention has no partials mode");

@@ -149,15 +149,31 @@ void run_with_workspace(const lbw_attn_params& p, const at::Tensor& q, Fn fn, Si
   check(fn(&p, ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(q)), what);
 }
 
+// The per-key score bias: fp32, contiguous, one value per key of the segments, on q's device.
+void set_key_bias(lbw_attn_params& p, const std::optional<at::Tensor>& key_bias,
+                  const at::Tensor& q) {
+  if (!key_bias.has_value()) return;
+  const at::Tensor& kb = *key_bias;
+  int64_t total = 0;
+  for (int i = 0; i < p.n_segments; ++i) total += p.seg[i].len;
+  TORCH_CHECK(kb.scalar_type() == at::kFloat && kb.is_contiguous() && kb.device() == q.device() &&
+                  kb.numel() == total,
+              "key_bias must be a contiguous fp32 tensor of ", total, " values (one per key) on "
+              "q's device");
+  p.key_bias = kb.data_ptr<float>();
+}
+
 void attention_out(const at::Tensor& q, at::TensorList k, at::TensorList v, int64_t kv_lo,
                    int64_t kv_hi, const std::optional<at::Tensor>& k_lens, double softmax_scale,
                    int64_t num_splits, const at::Tensor& out,
                    const std::optional<at::Tensor>& kv_lo_dev,
-                   const std::optional<at::Tensor>& kv_hi_dev) {
+                   const std::optional<at::Tensor>& kv_hi_dev,
+                   const std::optional<at::Tensor>& key_bias) {
   c10::DeviceGuard guard(q.device());
   lbw_attn_params p = base_params(q, k, v, kv_lo, kv_hi, softmax_scale, num_splits);
   set_out(p, out, q);
   set_k_lens(p, k_lens, q);
+  set_key_bias(p, key_bias, q);
   DevBounds db;
   db.set(p, kv_lo_dev, kv_hi_dev, q);
   run_with_workspace(p, q, lbw_attention_fwd, lbw_attention_workspace_size, "lbw_attention_fwd");
@@ -166,10 +182,11 @@ void attention_out(const at::Tensor& q, at::TensorList k, at::TensorList v, int6
 at::Tensor attention(const at::Tensor& q, at::TensorList k, at::TensorList v, int64_t kv_lo,
                      int64_t kv_hi, const std::optional<at::Tensor>& k_lens, double softmax_scale,
                      int64_t num_splits, bool out_fp32, const std::optional<at::Tensor>& kv_lo_dev,
-                     const std::optional<at::Tensor>& kv_hi_dev) {
+                     const std::optional<at::Tensor>& kv_hi_dev,
+                     const std::optional<at::Tensor>& key_bias) {
   at::Tensor out = new_out(q, out_fp32);
   attention_out(q, k, v, kv_lo, kv_hi, k_lens, softmax_scale, num_splits, out, kv_lo_dev,
-                kv_hi_dev);
+                kv_hi_dev, key_bias);
   return out;
 }
 
@@ -462,7 +479,8 @@ void kv_quant_fp8_(const at::Tensor& x, const at::Tensor& codes, const at::Tenso
 // ---- shapes for tracing (Meta / fake tensors): outputs only, no work
 using OptT = std::optional<at::Tensor>;
 at::Tensor attention_meta(const at::Tensor& q, at::TensorList, at::TensorList, int64_t, int64_t,
-                          const OptT&, double, int64_t, bool out_fp32, const OptT&, const OptT&) {
+                          const OptT&, double, int64_t, bool out_fp32, const OptT&, const OptT&,
+                          const OptT&) {
   return new_out(q, out_fp32);
 }
 at::Tensor cross_attention_meta(const at::Tensor& q, const at::Tensor&, const at::Tensor&,
@@ -497,7 +515,7 @@ at::Tensor attention_merge_meta(at::TensorList o, at::TensorList, at::TensorList
 }
 void attention_out_meta(const at::Tensor&, at::TensorList, at::TensorList, int64_t, int64_t,
                         const OptT&, double, int64_t, const at::Tensor&, const OptT&,
-                        const OptT&) {}
+                        const OptT&, const OptT&) {}
 void attention_merge_out_meta(at::TensorList, at::TensorList, at::TensorList,
                               const at::Tensor&) {}
 void qk_norm_rope_meta(const at::Tensor&, const std::optional<at::Tensor>&,
@@ -513,12 +531,13 @@ void kv_quant_fp8_meta(const at::Tensor&, const at::Tensor&, const at::Tensor&) 
 TORCH_LIBRARY(lbw, m) {
   // kv_lo_dev / kv_hi_dev: one-element integer tensors on q's device (the window read on the
   // device, no host sync); they narrow the host window kv_lo / kv_hi
+  // key_bias: fp32 [keys] score bias (natural log) shared by batch and heads
   m.def("attention(Tensor q, Tensor[] k, Tensor[] v, int kv_lo=0, int kv_hi=-1, "
         "Tensor? k_lens=None, float softmax_scale=0., int num_splits=0, bool out_fp32=False, "
-        "Tensor? kv_lo_dev=None, Tensor? kv_hi_dev=None) -> Tensor");
+        "Tensor? kv_lo_dev=None, Tensor? kv_hi_dev=None, Tensor? key_bias=None) -> Tensor");
   m.def("attention_out(Tensor q, Tensor[] k, Tensor[] v, int kv_lo, int kv_hi, Tensor? k_lens, "
         "float softmax_scale, int num_splits, Tensor(a!) out, Tensor? kv_lo_dev=None, "
-        "Tensor? kv_hi_dev=None) -> ()");
+        "Tensor? kv_hi_dev=None, Tensor? key_bias=None) -> ()");
   m.def("cross_attention(Tensor q, Tensor k, Tensor v, Tensor? k_lens=None, int n_distinct=-1, "
         "int kv_lo=0, int kv_hi=-1, float softmax_scale=0., bool out_fp32=False) -> Tensor");
   m.def("cross_attention_out(Tensor q, Tensor k, Tensor v, Tensor? k_lens, int n_distinct, "

@@ -7,7 +7,7 @@ when it is missing.
 """
 from .attention import (PRESCALED_SOFTMAX_SCALE, attention, attention_chain, attention_merge,
                         attention_merge_partials, attention_partial, attention_segments, prescaled_q_scale,
-                        cross_attention, exact_attention, exact_attention_chunks,
+                        cross_attention, cross_attention_dedup, exact_attention, exact_attention_chunks,
                         flash_attention, padding_start)
 from .chunked_kv_cache import (FlatKVCache, allocate_self_kv_chunks, allocate_self_kv_chunks_fp8,
                                chunk_routing, num_chunks)
@@ -19,7 +19,7 @@ from .rope import RopeTables, causal_rope_tables, rope_params, wan_rope_freqs
 
 __all__ = [
     "attention", "flash_attention", "exact_attention", "exact_attention_chunks",
-    "cross_attention", "padding_start", "attention_partial", "attention_merge",
+    "cross_attention", "cross_attention_dedup", "padding_start", "attention_partial", "attention_merge",
     "attention_merge_partials", "attention_chain", "attention_segments",
     "PRESCALED_SOFTMAX_SCALE", "prescaled_q_scale",
     "qk_norm_rope", "qk_norm_rope_", "qk_norm_rope3", "qk_norm_rope_t", "qk_norm_rope_t3",

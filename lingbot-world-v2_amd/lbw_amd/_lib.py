@@ -53,6 +53,7 @@ class AttnParams(ctypes.Structure):
         ("part_o", ctypes.c_void_p), ("part_m", ctypes.c_void_p), ("part_l", ctypes.c_void_p),
         ("out_dtype", ctypes.c_int32),
         ("kv_lo_dev", ctypes.c_void_p), ("kv_hi_dev", ctypes.c_void_p),
+        ("key_bias", ctypes.c_void_p),
     ]
 
 

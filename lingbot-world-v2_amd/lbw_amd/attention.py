@@ -23,7 +23,7 @@ import torch
 from . import _lib
 
 __all__ = ["attention", "flash_attention", "exact_attention", "exact_attention_chunks",
-           "cross_attention", "attention_partial", "attention_merge", "attention_merge_partials",
+           "cross_attention", "cross_attention_dedup", "attention_partial", "attention_merge", "attention_merge_partials",
            "attention_chain",
            "attention_segments", "window_from_mask", "PRESCALED_SOFTMAX_SCALE",
            "prescaled_q_scale"]
@@ -84,7 +84,8 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
                        k_lens: torch.Tensor | None = None, softmax_scale=None,
                        num_splits: int = 0, out: torch.Tensor | None = None,
                        cross: bool = False, n_distinct: int | None = None,
-                       out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+                       out_dtype: torch.dtype = torch.bfloat16,
+                       key_bias: torch.Tensor | None = None) -> torch.Tensor:
     """softmax(scale Q K^T) V over the windowed concatenation of KV ``segments``.
 
     q ``[B, Lq, N, 128]``; each segment is ``(k, v)`` with k/v ``[B, L_i, N, 128]`` (strided
@@ -96,7 +97,9 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
     ``n_distinct..`` identical rows, attended as one key of that multiplicity (exact).
     Returns bf16 ``[B, Lq, N, 128]`` (into ``out`` when given). ``out_dtype=torch.float32``
     (or an fp32 ``out``) returns the normalised output before its bf16 rounding, from the same
-    kernels and plan: a check of the kernels' own arithmetic."""
+    kernels and plan: a check of the kernels' own arithmetic. ``key_bias`` (fp32, one value per
+    key of the concatenation, shared by batch and heads) is added to the scaled scores:
+    softmax(scale Q K^T + bias) V."""
     ops = _lib.ops()
     device = q.device
     _check_4d("q", q, device)
@@ -111,6 +114,11 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
         raise ValueError(f"out_dtype {out_dtype}: bfloat16 or float32")
     if k_lens is not None:
         k_lens = k_lens.to(device=device, dtype=torch.int32).contiguous()
+    if key_bias is not None:
+        key_bias = key_bias.to(device=device, dtype=torch.float32).contiguous()
+        cross = False  # (the chunk kernel carries the bias; one pass for a short context)
+        if n_distinct is not None:
+            raise ValueError("n_distinct carries its own bias: pass one or the other")
     if cross:
         if len(ks) != 1:
             raise ValueError("cross-attention takes one KV segment")
@@ -124,8 +132,8 @@ def attention_segments(q: torch.Tensor, segments: Sequence, *, kv_lo=None, kv_hi
         return out
     if out is None:
         return ops.attention(q, ks, vs, lo, hi, k_lens, scale, int(num_splits),
-                             out_dtype == torch.float32, dlo, dhi)
-    ops.attention_out(q, ks, vs, lo, hi, k_lens, scale, int(num_splits), out, dlo, dhi)
+                             out_dtype == torch.float32, dlo, dhi, key_bias)
+    ops.attention_out(q, ks, vs, lo, hi, k_lens, scale, int(num_splits), out, dlo, dhi, key_bias)
     return out
 
 
@@ -227,6 +235,22 @@ def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16, n_distinct=None)
     if n_distinct is not None and k_lens is not None:
         raise ValueError("dedup reproduces the unmasked attention: pass k_lens or n_distinct")
     return attention_segments(q, [(k, v)], k_lens=k_lens, cross=True, n_distinct=n_distinct)
+
+
+def cross_attention_dedup(q, k, v, bias, kc, dtype=torch.bfloat16):
+    """attention.py:532-554 ``cross_attention_dedup``: q ``[1, Lq, N, D]`` against the first
+    ``kc`` keys of the cross cache with a per-key additive bias ``[kc]`` (natural log, the
+    log-multiplicity of cross_dedup_bias or any other), softmax(q k^T / sqrt(D) + bias) v.
+    k / v are ``[1, L, N, D]`` (token-major, or d-major K views) or the reference's N-major
+    cache as it is passed there, K ``[N, D, L]`` and V ``[N, L, D]`` (read in place).
+    ``dtype`` must be bf16, as for :func:`attention`."""
+    _check_dtype(dtype)
+    if k.dim() == 3 and v.dim() == 3:   # the reference's N-major cache itself: [N, D, L], [N, L, D]
+        k, v = k.permute(2, 0, 1)[None], v.permute(1, 0, 2)[None]
+    kc = int(kc)
+    if bias.numel() != kc:
+        raise ValueError(f"bias has {bias.numel()} values, kc = {kc}")
+    return attention_segments(q, [(k[:, :kc], v[:, :kc])], key_bias=bias.reshape(kc))
 
 
 def padding_start(k: torch.Tensor, v: torch.Tensor) -> int:
