@@ -150,3 +150,35 @@ def test_wan13b_480p_chunk_step_pipeline(lib):
     """1.3B 480p: 3-frame chunk (4680 q, start frame 6) over 6 cached frames + the chunk
     (14040 keys), 12 heads."""
     _pipeline(12, (3, 30, 52), 6, 9360, heads=[0, 6, 11], rows=256, seed=7, two_segments=False)
+
+
+def test_wan14b_720p_every_head_and_row(lib):
+    """The 14B 720p chunk call at full size over all 40 heads: 64 sampled rows of every head
+    (the last, partly filled q-tile's 16 rows among them) against the oracle; over all 3600 x 40
+    rows, the bf16 output equal to the fp32 output rounded once, and the 3-piece call (partials
+    merged in the kernel) within one bf16 step of the single-pass call."""
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments, prescaled_q_scale
+    H, Lq, LK = 40, 3600, 46800
+    g = torch.Generator(device=DEV).manual_seed(21)
+    q = (torch.randn(1, Lq, H, D, generator=g, device=DEV) * prescaled_q_scale(D)).to(torch.bfloat16)
+    k = torch.randn(1, LK, H, D, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(1, LK, H, D, generator=g, device=DEV).to(torch.bfloat16)
+    segs = [(k, v)]
+    out = attention_segments(q, segs, softmax_scale=PRESCALED_SOFTMAX_SCALE, num_splits=3)
+    o32 = attention_segments(q, segs, softmax_scale=PRESCALED_SOFTMAX_SCALE, num_splits=3,
+                             out_dtype=torch.float32)
+    one = attention_segments(q, segs, softmax_scale=PRESCALED_SOFTMAX_SCALE, num_splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(o32.to(torch.bfloat16), out)
+    d = (out.float() - one.float()).abs()
+    step = 2.0 ** -7 * one.float().abs().clamp_min(1.0)
+    assert bool((d <= step).all()), float((d / step).max())
+    sel = torch.cat([torch.randperm(Lq - 16, generator=torch.Generator().manual_seed(3))[:48],
+                     torch.arange(Lq - 16, Lq)]).sort().values
+    qs, ks, vs = q[:, sel].cpu(), k.cpu(), v.cpu()
+    for h in range(H):
+        ref = O.attention_ref(qs[:, :, h:h + 1], ks[:, :, h:h + 1], vs[:, :, h:h + 1],
+                              softmax_scale=LN2)
+        assert_parity(out[:, sel, h:h + 1], ref, f"head {h}")
+    print(f"40 heads x {sel.numel()} rows: parity; {Lq * H} rows: bf16 = round(fp32), "
+          f"max |3 pieces - 1 pass| = {float(d.max()):.3e}", flush=True)

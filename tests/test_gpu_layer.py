@@ -94,7 +94,8 @@ def test_windowed_flat_cache_evicts_with_sink(lib, max_att_frames):
 
 def test_chunked_cache_path_equals_flat(lib):
     """The chunked cache (3 slots of one 8 x 8 frame each) gives the flat cache's result: the
-    64-token chunks make both layouts walk the same key tiles in the same order."""
+    64-token chunks make both layouts walk the same key tiles in the same order; and each
+    chunk's output against the oracle's layer over the frames the chunks hold."""
     from lbw_amd import FlatKVCache, WanSelfAttention, allocate_self_kv_chunks
     g = torch.Generator().manual_seed(2)
     C, H, F = 512, 4, 8 * 8
@@ -103,12 +104,22 @@ def test_chunked_cache_path_equals_flat(lib):
     frames = [torch.randn(1, F, C, generator=g).to(torch.bfloat16).to(DEV) for _ in range(3)]
     flat = FlatKVCache(1, 3 * F, H, 128, device=DEV)
     chunks = allocate_self_kv_chunks(1, 1, F, H, 128, 3, device=DEV)[0]
+    f = {k: v.float() for k, v in ws.items()}
     for i, fr in enumerate(frames):
         a = layer.forward(fr, (1, 8, 8), i, flat, current_start=i * F)
         b = layer.forward_chunked(fr, (1, 8, 8), i, chunks, chunk_index=i)
         m = metrics(b, a)
         print(i, "identical" if torch.equal(a, b) else "differs", m)
         assert m["nonfinite"] == 0 and m["max_abs"] <= 1e-3, (i, m)
+        if i == 0:
+            continue
+        # the chunks before this one are the cache: frames 0 .. i-1 at start frame 0
+        xc = torch.cat([x.cpu() for x in frames[:i]], 1).float()
+        ref = O.self_attention_layer_ref(fr.cpu().float(), xc, f["wq"], f["bq"], f["wk"],
+                                         f["bk"], f["wv"], f["bv"], f["wo"], f["bo"], f["gq"],
+                                         f["gk"], heads=H, grid=(1, 8, 8), cache_grid=(i, 8, 8),
+                                         start_frame=i, cache_start_frame=0)
+        _check(b, ref, f"chunked cache, chunk {i}")
 
 
 def test_chunked_fp8_cache_path(lib):
