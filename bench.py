@@ -296,18 +296,27 @@ def other_configs(dev):
                      "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2),
                      "pct_hbm_peak": round(by / ms / 1e6 / PEAK_HBM_GBS * 100, 2)}
     del q, kx, vx
+    # q pre-scaled as the fused q/k kernel writes it (the folded softmax), as in the headline
+    # step; the same call on a plain-scaled q, and on a bf16 cache of the same keys
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, prescaled_q_scale
     q = rnd(1, 3600, 40, D)
+    qs = (q.float() * prescaled_q_scale(D)).to(torch.bfloat16)
     lk = 3600 * 25
-    k8 = quantize_kv_fp8(rnd(1, lk, 40, D))
-    v8 = quantize_kv_fp8(rnd(1, lk, 40, D))
+    kb, vb = rnd(1, lk, 40, D), rnd(1, lk, 40, D)
+    k8, v8 = quantize_kv_fp8(kb), quantize_kv_fp8(vb)
     o = torch.empty_like(q)
-    ms = _time_ms(lambda: attention_fp8kv(q, [(k8, v8)], out=o))
+    ms = _time_ms(lambda: attention_fp8kv(qs, [(k8, v8)], softmax_scale=PRESCALED_SOFTMAX_SCALE,
+                                          out=o))
+    ms_plain = _time_ms(lambda: attention_fp8kv(q, [(k8, v8)], out=o))
+    ms_bf16 = _time_ms(lambda: attention_segments(qs, [(kb, vb)],
+                                                  softmax_scale=PRESCALED_SOFTMAX_SCALE, out=o))
     fl = 4.0 * 3600 * lk * D * 40
     out["wan14b_720p_1f_over_24f_fp8kv"] = {
         "ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
         "pct_fp8_peak": round(fl / ms / 1e9 / PEAK_FP8_TFLOPS * 100, 2),
-        "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2)}
-    del q, k8, v8
+        "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2),
+        "ms_plain_scale_q": round(ms_plain, 4), "ms_bf16_cache_same_keys": round(ms_bf16, 4)}
+    del q, qs, kb, vb, k8, v8
     # fused q/k norm + RoPE with head-major d-major outputs [H, D, L] (q scaled by 1/sqrt(D)),
     # 14B 720p chunk; four input/output sets in turn so that the MALL does not serve the reads
     from lbw_amd import causal_rope_tables, qk_norm_rope_, wan_rope_freqs
@@ -467,20 +476,22 @@ def cross_workload():
 def fp8_workload():
     """The program the fp8-cache profiles run: 5 calls of the 14B 720p long-horizon chunk
     (3600 q x 40 heads over 90000 keys) on an fp8-e4m3 cache, then 5 on the same keys as a bf16
-    cache, on seeded inputs."""
+    cache, on seeded inputs, q pre-scaled (the folded softmax, as in the headline step)."""
     import torch
-    from lbw_amd import attention_fp8kv, attention_segments, quantize_kv_fp8
+    from lbw_amd import (PRESCALED_SOFTMAX_SCALE, attention_fp8kv, attention_segments,
+                         prescaled_q_scale, quantize_kv_fp8)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     g = torch.Generator(device=dev).manual_seed(0)
-    q = torch.randn(1, 3600, 40, D, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(1, 3600, 40, D, generator=g, device=dev)
+    q = (q * prescaled_q_scale(D)).to(torch.bfloat16)
     k = torch.randn(1, 90000, 40, D, generator=g, device=dev).to(torch.bfloat16)
     v = torch.randn(1, 90000, 40, D, generator=g, device=dev).to(torch.bfloat16)
     k8, v8 = quantize_kv_fp8(k), quantize_kv_fp8(v)
     for _ in range(5):
-        attention_fp8kv(q, [(k8, v8)])
+        attention_fp8kv(q, [(k8, v8)], softmax_scale=PRESCALED_SOFTMAX_SCALE)
     for _ in range(5):
-        attention_segments(q, [(k, v)])
+        attention_segments(q, [(k, v)], softmax_scale=PRESCALED_SOFTMAX_SCALE)
     torch.cuda.synchronize()
     print("fp8 workload done", flush=True)
 

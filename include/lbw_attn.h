@@ -156,7 +156,10 @@ int lbw_cross_attention_dedup_fwd(const lbw_attn_params* p, int64_t n_distinct, 
 
 /* fp8-e4m3 KV cache: K/V segments hold e4m3fn codes with per-(batch, head, 64-token block)
  * fp32 scales (lbw_kv_quant_fp8's layout); Q is given in bf16. Q K^T runs on the fp8 matrix
- * cores (each query split into two e4m3 operands that hold its bf16 values), P V in bf16. */
+ * cores (each query split into two e4m3 operands that hold its bf16 values) with K's scale as
+ * the product's exponent scale, P V in bf16 on V codes converted exactly at V's scale. The
+ * scales must be powers of two (lbw_kv_quant_fp8 writes them so): a row that reads a tile whose
+ * scale is not one comes out NaN. */
 int lbw_attention_fwd_fp8kv(const lbw_attn_params* p, void* workspace, size_t workspace_bytes,
                             void* stream);
 
@@ -216,7 +219,8 @@ int lbw_qk_norm_rope(const lbw_qk_norm_rope_params* p, void* stream);
 
 /* fp8-e4m3fn KV quantiser: x bf16 [B, L, H, D] (strided) -> codes uint8 [B, L, H, D]
  * (contiguous) and scales fp32 [B, H, ceil(L / block)] (contiguous). Per (b, h, block):
- * scale = amax / 448 (1 if amax == 0); code = rne_e4m3fn(x * (1 / scale)). */
+ * scale = the smallest power of two 2^k >= amax / 448, k >= -126 (1 if amax == 0);
+ * code = rne_e4m3fn(x * 2^-k). */
 int lbw_kv_quant_fp8(const void* x, int32_t batch, int64_t len, int32_t heads,
                      int32_t head_dim, int64_t s_b, int64_t s_l, int64_t s_h,
                      uint8_t* codes, float* scales, int32_t block, void* stream);

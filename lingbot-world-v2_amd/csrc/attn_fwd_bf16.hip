@@ -83,10 +83,11 @@ __device__ __forceinline__ void wait_vm(int n) {
 // S^T += K Q^T on the fp8 matrix cores: v_mfma_scale_f32_32x32x64_f8f6f4 with both operands
 // e4m3 (format 0). Operand byte j of lane (l32, h) is d = 64m + 16h + j (j < 16) or
 // 64m + 32 + 16h + (j - 16) (j >= 16) of d-half m, for the K row and the query column alike;
-// the query's operand carries the e8m0 scale `qscale` (2^(qscale - 127)), K's is 1 (127).
+// the operands carry the e8m0 scales `kscale` (K's block scale, a power of two) and `qscale`
+// (2^(qscale - 127)), so the product is the true score q . k.
 __device__ __forceinline__ floatx16 mfma_qk8(const i32x8& k, const i32x8& q, const floatx16& c,
-                                             int qscale) {
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(k, q, c, 0, 0, 0, 127, 0, qscale);
+                                             int kscale, int qscale) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(k, q, c, 0, 0, 0, kscale, 0, qscale);
 }
 
 // The query operand of the fp8 QK product: the lane's 64 bf16 values of its query (qf[4m + 2r +
@@ -235,15 +236,15 @@ __device__ void merge_unit(const AttnKernelArgs& a, int b, int h, int qt, int ro
   }
 }
 
-// FP8 = false: bf16 K/V, DMA'd straight into LDS. FP8 = true: e4m3 K/V codes with fp32 scales
-// per (batch, head, 64-token block). The K codes are copied into LDS as they are and S^T = K Q^T
+// FP8 = false: bf16 K/V, DMA'd straight into LDS. FP8 = true: e4m3 K/V codes with power-of-two
+// fp32 scales per (batch, head, 64-token block). The K codes are copied into LDS as they are and S^T = K Q^T
 // runs on the fp8 matrix cores, against Q split into two e4m3 operands (q8_split): four x64
 // MFMAs per 32-key sub-block instead of eight bf16 ones, half the K bytes in LDS and no K
 // conversion. The V codes and the tile's two scales go through a per-wave LDS staging slot
 // (copied two steps ahead); the wave that copied them converts its rows exactly to bf16 (every
-// e4m3 value is a bf16 value) into the bf16 V tile, so P stays bf16 in the PV product. The block
-// scales fold into the softmax (K's into the exponent's multiplier, V's into its addend as log2,
-// and out of the row sum).
+// e4m3 value times a power of two is a bf16 value) into the bf16 V tile, so P stays bf16 in the
+// PV product. The block scales stay out of the softmax: K's is the exponent scale of the fp8
+// product (whose result is then the true score), V's the scale of the exact conversion.
 // FOLD: scale * log2(e) == 1, i.e. q already carries log2(e)/sqrt(d) (a pre-scaled q, as the
 // fused q/k kernel writes it): the QK chain starts from -m instead of 0, so the MFMA result is
 // already the exponent of p and the softmax needs no per-score FMA (see the step).
@@ -263,7 +264,7 @@ __device__ void merge_unit(const AttnKernelArgs& a, int b, int h, int qt, int ro
 template <bool FP8, bool TRACK, bool FOLD, int SEGN, bool KDM = false, bool BIAS = false>
 __global__ void __launch_bounds__(NWAVE * 64, 1)
 attn_fwd_bf16_kernel(const AttnKernelArgs a) {
-  static_assert(!FOLD || (!FP8 && !TRACK), "the folded softmax is the plain bf16 form");
+  static_assert(!FOLD || !TRACK, "the folded softmax is the plain form");
   static_assert(!KDM || (!FP8 && SEGN == 0), "d-major K: bf16, general tile cursor");
   static_assert(!BIAS || (!FP8 && !TRACK && !FOLD && SEGN == 0), "key bias: plain bf16 form");
   constexpr int ESZ = FP8 ? 1 : 2;  // bytes per K/V element in HBM
@@ -621,32 +622,35 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
     }
   };
-  // this lane's 16 staged V codes of slot `slot` -> bf16 into V stage `stage` (row vrow8,
-  // logical chunks 2 vj8 and 2 vj8 + 1); the tile's block scales -> sk, sv
-  auto convert_v = [&](int slot, int stage, float& sk, float& sv) {
+  // this lane's 16 staged V codes of slot `slot` -> bf16 (times V's block scale, a power of two:
+  // exact) into V stage `stage` (row vrow8, logical chunks 2 vj8 and 2 vj8 + 1); K's block scale
+  // -> kse, as the e8m0 exponent of the fp8 product
+  auto convert_v = [&](int slot, int stage, int& kse) {
     const u32x4 x = lds_read_b128((int)raw_wave + slot * TILE8_B + 16 * lane);
     const u32x2 sc = lds_read_b64((int)sc_wave + slot * SC_SLOT_B);
+    // (a scale that is not a power of two, whose mantissa the exponent scale and the
+    // conversion would drop, turns into NaN: e8m0 0xff for K, a NaN factor for V)
+    const float sv = (sc[1] & 0x7fffffu) ? __uint_as_float(0x7fc00000u) : __uint_as_float(sc[1]);
     unsigned char* vd = lds + V_BASE + stage * TILE_B + vrow8 * ROWB;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       const uint32_t w0 = x[2 * hf], w1 = x[2 * hf + 1];
       const u32x4 y = {
-          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
-          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
-          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
-          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sv, false)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, sv, true)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sv, false)),
+          __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, sv, true))};
       *reinterpret_cast<u32x4*>(vd + (((2 * vj8 + hf) ^ swz(vrow8)) << 4)) = y;
     }
-    sk = __uint_as_float(sc[0]);
-    sv = __uint_as_float(sc[1]);
+    kse = (sc[0] & 0x7fffffu) ? 0xff : (int)((sc[0] >> 23) & 0xffu);
   };
 
   const int T = t1 - t0;
   if (T > 0) {
     int vr[NSTAGE];  // valid rows of tiles u .. u+NSTAGE-1 (u = the tile being softmaxed)
-    float skr[NSTAGE], svr[NSTAGE];  // fp8 block scales of the same tiles
+    int kser[NSTAGE];  // fp8: K's block scales of the same tiles (e8m0)
 #pragma unroll
-    for (int k = 0; k < NSTAGE; ++k) { vr[k] = ROWS_FULL; skr[k] = 1.0f; svr[k] = 1.0f; }
+    for (int k = 0; k < NSTAGE; ++k) { vr[k] = ROWS_FULL; kser[k] = 127; }
     i32x8 qh[2], ql[2];  // fp8: the query operands (hi, lo) of d-halves 0 and 1
     int sbh = 127, sbl = 127;  // and their e8m0 scales
     cursor_init<ESZ>(a, lo, hi, t0, b, h, cs);
@@ -684,7 +688,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     if constexpr (FP8) {
       // tile 0's V into stage 0 (read from the end of step 0 on), and the fp8 query operands
-      convert_v(0, 0, skr[0], svr[0]);
+      convert_v(0, 0, kser[0]);
       sbh = q8_split(qf, qh, ql);
       sbl = sbh - 4;
     }
@@ -744,8 +748,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
           load_k(std::integral_constant<int, 0>{}, m);
-          sA = mfma_qk8(k8f[m], qh[m], sA, sbh);
-          sA = mfma_qk8(k8f[m], ql[m], sA, sbl);
+          sA = mfma_qk8(k8f[m], qh[m], sA, kser[0], sbh);
+          sA = mfma_qk8(k8f[m], ql[m], sA, kser[0], sbl);
         }
         load_k(std::integral_constant<int, HALF8_B>{}, 0);
       } else {
@@ -767,13 +771,13 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         load_v(std::integral_constant<int, (NSTAGE - 1) * TILE_B + HALF_B>{}, i);
     }
 
-    // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow and,
-    // for fp8, block scales sk / sv) into p_out, O += V^T p_in^T from LDS offset VO,
-    // s_out = K Q^T from LDS offset KO. KPRE / VPRE: the first K / V fragments were read by the
+    // One pipeline step: softmax of s_in (sub-block `kb` of a tile with valid rows vrow) into
+    // p_out, O += V^T p_in^T from LDS offset VO, s_out = K Q^T from LDS offset KO (fp8: with K's
+    // block scale kse, the e8m0 exponent of s_out's tile). KPRE / VPRE: the first K / V fragments were read by the
     // previous step; NKO / NVO (>= 0): read the next step's first fragments from there.
     auto step = [&](auto koff_c, auto voff_c, auto kpre_c, auto vpre_c, auto nko_c, auto nvo_c,
                     floatx16& s_in, floatx16& s_out, u32x4 (&p_in)[2], u32x4 (&p_out)[2], int kb,
-                    int vrow, float sk, float sv) {
+                    int vrow, int kse) {
       constexpr bool KPRE = decltype(kpre_c)::value, VPRE = decltype(vpre_c)::value;
       constexpr int NKO = decltype(nko_c)::value, NVO = decltype(nvo_c)::value;
       if constexpr (!KPRE) {
@@ -814,19 +818,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       bool move = false;
       float alpha = 1.0f;
       if constexpr (TRACK) {
-        if constexpr (FP8) {
-          // fp8 scores are q . k_code; the true score is that times the K block scale
-          float mx = s_in[0];
+        // lanes l and l^32 hold the same query's running max: fold it in before the exchange
+        float mx = m_true;
 #pragma unroll
-          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
-          m_true = fmaxf(m_true, wave_max_xor32(mx) * sk);
-        } else {
-          // lanes l and l^32 hold the same query's running max: fold it in before the exchange
-          float mx = m_true;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
-          m_true = wave_max_xor32(mx);
-        }
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
+        m_true = wave_max_xor32(mx);
         // Every lane sees the same valid keys, so m_true is -inf in all lanes or in none, and
         // a move never selects -inf.
         move = __any(m_true > m_used + tau_raw);
@@ -836,10 +832,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       }
       // The reference starts at M_INIT, a finite stand-in for -inf, so no step needs an
       // infinity case: masked scores (-inf) give p = 0, and the first valid score moves it.
-      // p = exp2(s_code sk c - m c), times sv for fp8 (V's scale, so that P^T V_code = P^T V)
-      const float cm = FP8 ? c * sk : c;
-      const float lsv = FP8 ? __builtin_amdgcn_logf(sv) : 0.0f;
-      float ca = lsv - m_used * c;
+      // p = exp2(s c - m c)
+      float ca = -m_used * c;
       // MFMAs of the neighbouring sub-blocks
       if constexpr (FOLD) {
         s_out = cinit;
@@ -865,7 +859,8 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
           // QK on the fp8 cores at even i: (d-half i / 4) x (hi, lo)
           if ((i & 1) == 0) {
             const int m = i >> 2;
-            s_out = (i & 2) ? mfma_qk8(k8f[m], ql[m], s_out, sbl) : mfma_qk8(k8f[m], qh[m], s_out, sbh);
+            s_out = (i & 2) ? mfma_qk8(k8f[m], ql[m], s_out, kse, sbl)
+                            : mfma_qk8(k8f[m], qh[m], s_out, kse, sbh);
           }
         } else {
           s_out = mfma32x32x16(kf[i % KR], qf[i], s_out);
@@ -879,14 +874,13 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         for (int m = 0; m < 2; ++m) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float x0 = fast_exp2(FOLD ? s_in[8 * m + 2 * e] : __builtin_fmaf(s_in[8 * m + 2 * e], cm, ca));
+            const float x0 = fast_exp2(FOLD ? s_in[8 * m + 2 * e] : __builtin_fmaf(s_in[8 * m + 2 * e], c, ca));
             const float x1 = fast_exp2(FOLD ? s_in[8 * m + 2 * e + 1]
-                                            : __builtin_fmaf(s_in[8 * m + 2 * e + 1], cm, ca));
+                                            : __builtin_fmaf(s_in[8 * m + 2 * e + 1], c, ca));
             p_out[m][e] = pack_bf16x2(x0, x1);
             l = (m == 0 && e == 0) ? x0 + x1 : l + (x0 + x1);
           }
         }
-        if constexpr (FP8) l *= __builtin_amdgcn_rcpf(sv);
         return l;
       };
       float ls = exps();
@@ -903,15 +897,29 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         if constexpr (FP8) {
           // the QK product (even i) and the PV product, 2 VALU after each, and between them
           // the LDS reads: K operands at i = 0 and 4, V fragments V_AHEAD pairs ahead
+          // (folded: exponentials named as transcendentals, which the VALU class does not take:
+          // per MFMA pair 1 + 1 with 1 + 2 VALU ops, after a lone PV MFMA 2 with 3; measured
+          // 2.7 % faster than one of each after every MFMA)
           const int nds = ((i == 0 || (i == 4 && NKO >= 0)) ? 2 : 0) + (rv ? 2 : 0);
           if (i % 2 == 0) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            if constexpr (FOLD) __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, FOLD ? 1 : 2, 0);
           }
           if (nds == 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
           else if (nds == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          if constexpr (FOLD) {
+            if (i % 2 == 0) {
+              __builtin_amdgcn_sched_group_barrier(0x400, 1, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+            } else {
+              __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);
+              __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            }
+          } else {
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+          }
           continue;
         }
         if constexpr (FOLD) {
@@ -986,12 +994,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
 #pragma unroll
           for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[r]);
           mx = wave_max_xor32(mx);
-          if constexpr (FP8) mx *= sk;
           const float m_new = fmaxf(mx, m_used);
           alpha = fast_exp2((m_used - m_new) * c);
           m_used = m_new;
           move = true;
-          ca = lsv - m_new * c;
+          ca = -m_new * c;
           // O (with this step's PV of the previous sub-block, at the old reference) and the
           // row sum move now
           scale_acc(oacc, alpha);
@@ -1021,7 +1028,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
       constexpr int SP = (ST + NSTAGE - 1) % NSTAGE;  // stage of tile u-1
       constexpr int SN = (ST + 1) % NSTAGE;           // stage of tile u+1
       const int vrow = vr[0];
-      const float sk = skr[0], sv = svr[0];
+
       if constexpr (FP8) {
         // Copies in flight per lane, in issue order: staged V of tile u+1 (2, issued at the
         // start of tile u-1), K of tile u+1 (1, after tile u-1's barrier). Tile u+1's V goes
@@ -1029,7 +1036,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         // before the next one. Then tile u+2's V and scales into the slot tile u's left.
         if (u + 1 < T) {
           wait_vm(1);
-          convert_v((u + 1) & 1, SN, skr[1], svr[1]);
+          convert_v((u + 1) & 1, SN, kser[1]);
         }
         if (u + 2 < T) vr[2] = SEGN > 0 ? issue_raw1(u & 1, u + 2) : issue_raw(u & 1);
       }
@@ -1039,7 +1046,7 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         step(std::integral_constant<int, ST * KT_B + KH_B>{},
              std::integral_constant<int, SP * TILE_B + HALF_B>{}, std::true_type{},
              std::true_type{}, std::integral_constant<int, -1>{},
-             std::integral_constant<int, ST * TILE_B>{}, sA, sB, pA, pB, 0, vrow, sk, sv);
+             std::integral_constant<int, ST * TILE_B>{}, sA, sB, pA, pB, 0, vrow, kser[0]);
       if constexpr (FP8) {
         if (u + 1 < T) wait_vm(u + 2 < T ? 2 : 0);  // tile u+1's K (tile u+2's V may be in flight)
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V conversion's writes are done
@@ -1059,12 +1066,11 @@ attn_fwd_bf16_kernel(const AttnKernelArgs a) {
         step(std::integral_constant<int, SN * KT_B>{},
              std::integral_constant<int, ST * TILE_B>{}, std::false_type{}, std::true_type{},
              std::integral_constant<int, SN * KT_B + KH_B>{},
-             std::integral_constant<int, ST * TILE_B + HALF_B>{}, sB, sA, pB, pA, 1, vrow, sk, sv);
+             std::integral_constant<int, ST * TILE_B + HALF_B>{}, sB, sA, pB, pA, 1, vrow, kser[1]);
 #pragma unroll
       for (int k = 0; k < NSTAGE - 1; ++k) {
         vr[k] = vr[k + 1];
-        skr[k] = skr[k + 1];
-        svr[k] = svr[k + 1];
+        kser[k] = kser[k + 1];
       }
     };
 
@@ -1282,8 +1288,10 @@ hipError_t launch_attn_fwd(const AttnKernelArgs& a, hipStream_t stream) {
 
 hipError_t launch_attn_fwd_fp8(const AttnKernelArgs& a, hipStream_t stream) {
   if (a.track_max) return launch<true, true>(a, stream);
-  return index_segments(a) == 1 ? launch<true, false, false, 1>(a, stream)
-                                : launch<true, false>(a, stream);
+  const bool one = index_segments(a) == 1;
+  if (a.scale_log2 == 1.0f)  // a pre-scaled q: the folded softmax
+    return one ? launch<true, false, true, 1>(a, stream) : launch<true, false, true>(a, stream);
+  return one ? launch<true, false, false, 1>(a, stream) : launch<true, false>(a, stream);
 }
 
 }  // namespace lbw

@@ -1,9 +1,12 @@
 // fp8-e4m3fn KV-cache quantiser (gfx950). No reference counterpart: the format is defined
 // here. Per (batch, head, block of `block` tokens by absolute index in the buffer):
 //   amax  = max |x| over the block's tokens and all head_dim features (fp32)
-//   scale = amax / 448, or 1 when amax == 0
-//   inv   = 1 / scale
+//   scale = the smallest power of two 2^k >= amax / 448 (k >= -126), or 1 when amax == 0
+//   inv   = 1 / scale = 2^-k (exact)
 //   code  = round_to_nearest_even_e4m3fn(x * inv)
+// Power-of-two scales make a code times its scale exact in bf16: the attention kernel applies
+// K's scale as the exponent scale of its fp8 matrix-core product and V's in the exact
+// conversion of the codes to bf16, so neither enters the softmax arithmetic.
 // One workgroup per (b, h, block): the block's 64 x 128 bf16 values are read once into
 // registers (16-byte loads, 16 lanes per token row), reduced to amax, encoded and written.
 // Workgroups are numbered with (b, h) fastest.
@@ -74,8 +77,17 @@ kv_quant_fp8_kernel(const KvQuantArgs a) {
   if ((t & 63) == 0) red[t >> 6] = amax;
   __syncthreads();
   amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float scale = amax > 0.0f ? amax / 448.0f : 1.0f;
-  const float inv = 1.0f / scale;
+  // amax = m 2^E, m in [1, 2): amax / 2^k <= 1.75 * 2^8 from k = E - 8 on when m <= 1.75
+  // (mantissa field <= 0x600000), else from k = E - 7; a subnormal amax gets k = -126
+  int k = 0;
+  if (amax > 0.0f) {
+    const uint32_t u = __float_as_uint(amax);
+    const int eb = (int)(u >> 23);
+    k = eb == 0 ? -126 : eb - 127 - ((u & 0x7fffffu) <= 0x600000u ? 8 : 7);
+    k = k < -126 ? -126 : k;
+  }
+  const float scale = __uint_as_float((uint32_t)(127 + k) << 23);
+  const float inv = __uint_as_float((uint32_t)(127 - k) << 23);
   if (t == 0) a.scales[bh * a.nblk + blk] = scale;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {

@@ -3,8 +3,11 @@
 No reference counterpart (the reference keeps bf16 caches; its nearest relative is the
 delayed fp8 K dequant of kernels/attention_cte_lb.py:645-647). Format: e4m3fn codes in the
 cache's own ``[B, L, N, D]`` layout, plus fp32 scales ``[B, N, ceil(L/64)]`` per
-(batch, head, 64-token block by index within the buffer): scale = amax/448 (1 for an
-all-zero block), code = round_to_nearest_even(x / scale).
+(batch, head, 64-token block by index within the buffer): scale = the smallest power of two
+>= amax/448 (1 for an all-zero block), code = round_to_nearest_even(x / scale). The attention
+reads only power-of-two scales (rows that read any other come out NaN): K's scale is the
+exponent scale of the fp8 matrix-core product and V's the scale of the codes' exact conversion
+to bf16, so neither enters the softmax.
 """
 from __future__ import annotations
 
@@ -52,9 +55,10 @@ def attention_fp8kv(q: torch.Tensor, segments, *, kv_lo=None, kv_hi=None, softma
 
     Q K^T runs on the fp8 matrix cores: the K codes go to LDS as they are, and each query is
     split into two e4m3 operands (hi + lo / 16, times a power of two per query) that hold its
-    bf16 values. The V codes are converted exactly to bf16 (every e4m3 value is a bf16 value) and
-    P V runs on the bf16 matrix cores. The K block scale folds into the softmax exponent's
-    multiplier and the V block scale into its addend (and out of the row sum).
+    bf16 values, with K's block scale (a power of two) as the product's exponent scale. The V
+    codes are converted exactly to bf16 at V's block scale and P V runs on the bf16 matrix
+    cores. A q pre-scaled by ``prescaled_q_scale`` with ``softmax_scale=PRESCALED_SOFTMAX_SCALE``
+    takes the folded softmax, as in ``attention_segments``.
     ``out_dtype=torch.float32`` returns the output before its bf16 rounding."""
     ops = _lib.ops()
     device = q.device

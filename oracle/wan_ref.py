@@ -375,9 +375,12 @@ def quantize_kv_fp8(x: torch.Tensor, block: int = 64):
     Per (batch, head, block of ``block`` tokens by absolute index within the buffer):
 
         amax  = max |x| over the block's tokens and all D   (fp32)
-        scale = amax / 448, or 1 when amax == 0             (fp32 division)
-        inv   = 1 / scale                                   (fp32 division)
-        code  = e4m3fn_rne(x * inv)                         (fp32 multiply, then RNE)
+        scale = the smallest power of two 2^k >= amax / 448 (k >= -126), or 1 when amax == 0
+        inv   = 1 / scale = 2^-k                            (exact)
+        code  = e4m3fn_rne(x * inv)                         (exact multiply, then RNE)
+
+    The scales are fp32 powers of two, so the block's largest magnitude maps into (224, 448]
+    and a code times its scale is exact in bf16 and fp32 alike.
     """
     B, L, H, D = x.shape
     nb = (L + block - 1) // block
@@ -385,7 +388,11 @@ def quantize_kv_fp8(x: torch.Tensor, block: int = 64):
     pad = nb * block - L
     xp = torch.cat([xf, torch.zeros(B, pad, H, D)], 1) if pad else xf
     amax = xp.abs().view(B, nb, block, H, D).amax(dim=(2, 4)).permute(0, 2, 1).contiguous()
-    scale = torch.where(amax > 0, amax / torch.tensor(FP8_E4M3_MAX), torch.ones_like(amax))
+    # amax = m 2^e with m in [1, 2) (frexp: mant = m / 2 in [0.5, 1), ex = e + 1):
+    # m 2^(e - k) <= 1.75 * 2^8 holds from k = e - 8 on when m <= 1.75, else from k = e - 7
+    mant, ex = torch.frexp(amax)
+    k = torch.where(mant <= 0.875, ex - 9, ex - 8).clamp(min=-126)
+    scale = torch.where(amax > 0, torch.ldexp(torch.ones_like(amax), k.float()), torch.ones_like(amax))
     inv = torch.tensor(1.0, dtype=torch.float32) / scale                    # [B, H, nb]
     inv_tok = inv.permute(0, 2, 1).repeat_interleave(block, dim=1)[:, :L]   # [B, L, H]
     codes = fp8_e4m3_encode(xf * inv_tok.unsqueeze(-1))

@@ -9,9 +9,9 @@ the attention arithmetically (the oracle's e4m3 quantiser for the cache, then th
 P rounded as each design rounds it) and show what the two alternatives cost:
   - q as one e4m3 operand per query (scale 2^(floor(log2 max|q|) - 7), as the kernel's split
     uses): cosine below the 0.999 bar in both input families;
-  - P as e4m3 codes of p * 2^3 (times the mantissa of V's block scale, folded in so that the
-    product with the V codes carries V's scale): below the bar without outliers, and with them
-    left with a fraction of the current design's margin;
+  - P as e4m3 codes of p * 2^3 (times the mantissa of V's block scale, which is 1 for the
+    quantiser's power-of-two scales): below the bar without outliers, and with them left with
+    a fraction of the current design's margin;
 while the kernel's own design clears the bar in both. The GPU tests hold the kernel itself to
 its arithmetic bound (tests/test_gpu_fp8.py, tests/test_gpu_fp8_random.py).
 """

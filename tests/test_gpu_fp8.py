@@ -189,6 +189,63 @@ def test_fp8_kernel_arithmetic_fp32(lib, Lq, H, lk, window, splits):
     assert rel_l1 <= 4e-3
 
 
+@pytest.mark.parametrize("n_segs,splits", [(1, 0), (1, 3), (2, 0), (2, 2)])
+def test_fp8_prescaled_q_folded(lib, n_segs, splits):
+    """A q pre-scaled by log2(e)/sqrt(d) with softmax scale ln 2 takes the folded fp8 instances
+    (one segment: tile copies addressed by index; two: the general cursor): the fp32 output
+    against the oracle on the dequantised K/V within the kernel's arithmetic bound, and within
+    one bf16 step of the plain fp8 kernel on the same q."""
+    import math
+    from lbw_amd import (PRESCALED_SOFTMAX_SCALE, attention_fp8kv, prescaled_q_scale,
+                         quantize_kv_fp8)
+    g = torch.Generator().manual_seed(31 + n_segs + splits)
+    H, Lq = 3, 290
+    lens = (1300,) if n_segs == 1 else (640, 130)
+    q = _wide_q(Lq, H, g)
+    qs = (q.float() * prescaled_q_scale(128)).to(torch.bfloat16)
+    segs, kds, vds = [], [], []
+    for L in lens:
+        k = _outliers(torch.randn(1, L, H, 128, generator=g), g).to(torch.bfloat16)
+        v = _outliers(torch.randn(1, L, H, 128, generator=g), g).to(torch.bfloat16)
+        kq, vq = quantize_kv_fp8(k.to(DEV)), quantize_kv_fp8(v.to(DEV))
+        segs.append((kq, vq))
+        kds.append(O.dequantize_kv_fp8(kq.codes.cpu(), kq.scales.cpu()))
+        vds.append(O.dequantize_kv_fp8(vq.codes.cpu(), vq.scales.cpu()))
+    kd, vd = torch.cat(kds, 1), torch.cat(vds, 1)
+    print(f"case segs={lens} splits={splits}", flush=True)
+    out = attention_fp8kv(qs.to(DEV), segs, softmax_scale=PRESCALED_SOFTMAX_SCALE,
+                          num_splits=splits, out_dtype=torch.float32)
+    plain = attention_fp8kv(qs.to(DEV), segs, softmax_scale=math.log(2.0) + 1e-7,
+                            num_splits=splits, out_dtype=torch.float32)
+    ref = O.attention_ref(qs, kd, vd, softmax_scale=math.log(2.0))
+    bound = _row_bound(vd, _score_err(qs, kd, math.log(2.0)))
+    err = (out.cpu() - ref).abs().amax(-1)
+    print(f"  worst err/bound {float((err / bound).max()):.3f}")
+    assert bool((err <= bound).all())
+    d = (out - plain).abs().max().item()
+    assert d <= 2.0 ** -7 * max(1.0, float(plain.abs().max())), d
+
+
+def test_fp8_scales_not_powers_of_two_give_nan(lib):
+    """The attention reads power-of-two block scales only: a tile whose K or V scale is not one
+    turns the rows that read it into NaN instead of a silently wrong result."""
+    from lbw_amd import attention_fp8kv, quantize_kv_fp8
+    from lbw_amd.fp8 import Fp8KV
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(1, 70, 2, 128, generator=g).to(torch.bfloat16).to(DEV)
+    k = torch.randn(1, 200, 2, 128, generator=g).to(torch.bfloat16).to(DEV)
+    kq, vq = quantize_kv_fp8(k), quantize_kv_fp8(k)
+    good = attention_fp8kv(q, [(kq, vq)])
+    assert bool(torch.isfinite(good).all())
+    for which in ("k", "v"):
+        ks, vs = kq.scales.clone(), vq.scales.clone()
+        (ks if which == "k" else vs)[0, 1, 2] *= 1.5      # head 1, block 2 (keys 128..191)
+        out = attention_fp8kv(q, [(Fp8KV(kq.codes, ks), Fp8KV(vq.codes, vs))])
+        torch.cuda.synchronize()
+        assert bool(torch.isnan(out[:, :, 1]).all()), which
+        assert torch.equal(out[:, :, 0], good[:, :, 0]), which
+
+
 def test_fp8_partials_capi_match_oracle(lib):
     """The unnormalised partials (cte_partial contract: O and l relative to the row max m of the
     scaled scores) of the fp8 entry point, called through the C ABI, against the oracle on the

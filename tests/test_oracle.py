@@ -355,8 +355,20 @@ def test_fp8_quantizer_round_trip_and_scale_layout():
     x[0, 70, 1, 5] = 40.0                                       # an outlier in block 1, head 1
     codes, sc = O.quantize_kv_fp8(x, block=64)
     assert sc.shape == (1, 3, 3)
-    # the block's absolute max maps to code +-448
-    assert codes[0, 70, 1, 5] == 0x7E and torch.isclose(sc[0, 1, 1], torch.tensor(40.0 / 448))
+    # scales are the smallest powers of two with amax / scale <= 448: 40 -> 2^-3, 40 / 2^-3 =
+    # 320 = 1.25 * 2^8, e4m3 code 0x7A (exponent field 15, mantissa 010)
+    assert sc[0, 1, 1] == 0.125 and codes[0, 70, 1, 5] == 0x7A
+    mant, _ = torch.frexp(sc)
+    assert torch.all(mant == 0.5)                                # powers of two
+    amax = x.abs().view(1, 150, 3, 16)
+    amax = torch.cat([amax, torch.zeros(1, 42, 3, 16)], 1).view(1, 3, 64, 3, 16).amax(dim=(2, 4))
+    ratio = amax.permute(0, 2, 1) / sc
+    assert torch.all(ratio <= 448) and torch.all(ratio > 224)   # the smallest such power
+    # the edges: amax = 448 * 2^k -> scale 2^k exactly; just above -> 2^(k+1)
+    for v, want in ((448.0 * 2.0 ** -5, 2.0 ** -5), (448.0 * 2.0 ** -5 * (1 + 2.0 ** -20), 2.0 ** -4),
+                    (448.0, 1.0), (1.0, 2.0 ** -8), (1.75, 2.0 ** -8), (1.75 * (1 + 2.0 ** -20), 2.0 ** -7)):
+        _, s1 = O.quantize_kv_fp8(torch.full((1, 64, 1, 4), v))
+        assert float(s1[0, 0, 0]) == want, (v, float(s1[0, 0, 0]), want)
     deq = O.dequantize_kv_fp8(codes, sc)
     s_tok = sc.permute(0, 2, 1).repeat_interleave(64, 1)[:, :150].unsqueeze(-1)
     # RNE error bound: half a step of 2^-3 relative for normals, 2^-10 * scale for subnormals
