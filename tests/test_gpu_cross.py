@@ -80,6 +80,49 @@ def test_cross_rounds_across_workgroups_fp32(lib, H, Lq):
         assert err <= bound, (h, err, bound)
 
 
+@pytest.mark.parametrize("B,Lq,H,L,window", [
+    (1, 256, 1, 321, None),
+    (2, 300, 3, 384, None),
+    (1, 513, 2, 385, None),
+    (1, 64, 5, 512, None),
+    (2, 1000, 3, 512, (20, 470)),    # a 450-key window
+    (1, 100, 7, 450, None),
+])
+def test_cross_long_unmasked_context(lib, B, Lq, H, L, window):
+    """Unmasked contexts longer than the 320 resident keys (up to the reference's padded 512)
+    run the chunk kernel as one pass: bf16 bar, and the fp32 output within the kernel's
+    arithmetic bound and equal to the bf16 output before its rounding."""
+    from lbw_amd import attention_segments, cross_attention
+    q, k, v = _qkv(B, Lq, H, L, seed=3 * Lq + L + H, qgain=2.0)
+    lo, hi = (None, None) if window is None else window
+    print(f"case B={B} Lq={Lq} H={H} L={L} window={window}", flush=True)
+    if window is None:
+        out = cross_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    else:
+        out = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV))], kv_lo=lo, kv_hi=hi,
+                                 cross=True)
+    ref = O.attention_ref(q, k, v, kv_lo=lo, kv_hi=hi)
+    assert_parity(out, ref, "long context")
+    o32 = attention_segments(q.to(DEV), [(k.to(DEV), v.to(DEV))], kv_lo=lo, kv_hi=hi, cross=True,
+                             out_dtype=torch.float32)
+    a, b = (0, L) if window is None else window
+    err = float((o32.cpu() - ref).abs().max())
+    assert err <= _kernel_bound(v[:, a:b]), err
+    assert torch.equal(o32.to(torch.bfloat16), out)
+
+
+def test_cross_dedup_past_the_resident_keys(lib):
+    """The exact dedup over a context whose distinct rows end past the resident chunk (400 of
+    512: the distinct rows and the weighted identical ones up to their tile's end, 448 keys)
+    equals the full-context oracle."""
+    from lbw_amd import cross_attention
+    q, k, v = _qkv(1, 700, 3, 512, seed=77)
+    k[:, 400:] = k[:, 511:]
+    v[:, 400:] = v[:, 511:]
+    out = cross_attention(q.to(DEV), k.to(DEV), v.to(DEV), n_distinct=400)
+    assert_parity(out, O.attention_ref(q, k, v), "dedup past 320")
+
+
 def test_cross_window_and_strided_views(lib):
     """A key window [lo, hi) on a context held as column views of a fused [L, 2, H, D] buffer,
     q and out as strided views; bf16 output."""
