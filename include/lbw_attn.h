@@ -38,7 +38,8 @@
 extern "C" {
 #endif
 
-#define LBW_ABI_VERSION 3
+/* 4: the fp8 entry point reads power-of-two block scales only (lbw_kv_quant_fp8 writes them). */
+#define LBW_ABI_VERSION 4
 #define LBW_MAX_KV_SEGMENTS 8
 #define LBW_FP8_BLOCK 64
 

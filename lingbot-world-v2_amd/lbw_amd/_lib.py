@@ -17,7 +17,7 @@ OPS_PATH = os.path.join(_HERE, "liblbw_torch.so")
 
 MAX_KV_SEGMENTS = 8
 FP8_BLOCK = 64
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OUT_BF16 = 0
 OUT_FP32 = 1

@@ -35,7 +35,8 @@ def test_library_exports_every_declared_symbol():
     for name in _header_functions():
         assert hasattr(lib, name), name
     lib.lbw_abi_version.restype = ctypes.c_int
-    assert lib.lbw_abi_version() == 3
+    from lbw_amd import _lib
+    assert lib.lbw_abi_version() == _lib.ABI_VERSION == 4
 
 
 def _header_struct_fields(name):
