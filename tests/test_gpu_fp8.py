@@ -46,6 +46,30 @@ def test_quantizer_rounding_edges(lib):
     assert torch.equal(q.codes.cpu(), codes) and torch.equal(q.scales.cpu(), scales)
 
 
+def test_quantizer_power_of_two_scale_edges(lib):
+    """Block scales at their edges, bit-exact against the oracle: block maxima of exactly
+    448 * 2^k (scale 2^k, code 448) and one bf16 step above (scale 2^(k+1)), mantissas at and
+    past 1.75, a bf16 subnormal maximum (scale clamped to 2^-126), an all-zero block (scale 1);
+    every scale a power of two."""
+    from lbw_amd import quantize_kv_fp8
+    maxima = [448.0, 448.0 * 2.0 ** -5, 1.75, 1.7578125, 1.0, 0.9921875, 3.0e4, 2.0 ** -130, 0.0,
+              448.0 * 2.0 ** 3, 1.0e-3]
+    x = torch.zeros(1, 64 * len(maxima), 2, 128)
+    g = torch.Generator().manual_seed(3)
+    for i, m in enumerate(maxima):
+        blk = torch.rand(64, 2, 128, generator=g) * 2 - 1
+        x[0, 64 * i:64 * (i + 1)] = blk * m * 0.99
+        x[0, 64 * i + 5, :, 7] = m
+    x = x.to(torch.bfloat16)
+    q = quantize_kv_fp8(x.to(DEV))
+    codes, scales = O.quantize_kv_fp8(x.float())
+    assert torch.equal(q.scales.cpu(), scales) and torch.equal(q.codes.cpu(), codes)
+    mant, _ = torch.frexp(scales)
+    assert torch.all(mant == 0.5)
+    assert float(scales[0, 0, 0]) == 1.0 and float(scales[0, 0, 1]) == 2.0 ** -5
+    assert float(scales[0, 0, 7]) == 2.0 ** -126 and float(scales[0, 0, 8]) == 1.0
+
+
 @pytest.mark.parametrize("Lq,H,lk,window", [(300, 2, 2000, None), (100, 3, 777, (13, 700))])
 def test_fp8_attention_cosine(lib, Lq, H, lk, window):
     from lbw_amd import attention_fp8kv, quantize_kv_fp8
