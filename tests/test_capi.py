@@ -97,16 +97,19 @@ def _header_struct(name, known):
     return type(name, (ctypes.Structure,), {"_fields_": fields})
 
 
+GUIDE = os.path.join(ROOT, "INTEGRATION.md")   # the integration guide a maintainer follows
+
+
 def _integration_stub():
-    """The Seg and Params classes of the ctypes stub in INTEGRATION.md, executed as written."""
+    """The Seg and Params classes of the integration guide's ctypes stub, executed as written."""
     import ast
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    text = open(GUIDE).read()
     blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
     block = next(b for b in blocks if "class Params(ctypes.Structure)" in b)
     tree = ast.parse(block)
     classes = [n for n in tree.body if isinstance(n, ast.ClassDef)]
     ns = {"ctypes": ctypes}
-    exec(compile(ast.Module(body=classes, type_ignores=[]), "INTEGRATION.md", "exec"), ns)
+    exec(compile(ast.Module(body=classes, type_ignores=[]), GUIDE, "exec"), ns)
     return ns["Seg"], ns["Params"]
 
 
@@ -116,7 +119,7 @@ def _layout(struct):
 
 
 def test_integration_stub_matches_header():
-    """The binding INTEGRATION.md shows a maintainer has every field of the header's structs,
+    """The binding the integration guide shows a maintainer has every field of the header's structs,
     in order, at the same offsets and sizes: a stub missing a trailing field would let the
     library read past the caller's struct."""
     seg_h = _header_struct("lbw_kv_segment", {})
@@ -127,7 +130,7 @@ def test_integration_stub_matches_header():
     assert ctypes.sizeof(par_d) == ctypes.sizeof(par_h)
     from lbw_amd import _lib
     assert _layout(_lib.AttnParams) == _layout(par_h)
-    assert "lbw_abi_version() == %d" % _lib.ABI_VERSION in open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    assert "lbw_abi_version() == %d" % _lib.ABI_VERSION in open(GUIDE).read()
 
 
 def test_entry_points_reject_bad_arguments_without_gpu():
