@@ -264,22 +264,32 @@ def other_configs(dev):
     """The other workload shapes of this path, timed once each after the headline step (not
     part of `value`): 1.3B 480p 3-frame chunk over 6 cached frames, 14B 480p 3-frame chunk over
     18 cached frames, its cross-attention to a 512-token context (300 valid), and the 14B 720p
-    long-horizon chunk over an fp8-e4m3 cache of 24 frames + the chunk."""
+    long-horizon chunk over an fp8-e4m3 cache of 24 frames + the chunk. The self-attention
+    calls take q pre-scaled as the layer pipeline's fused q/k kernel writes it, with the
+    plain-scaled call beside it."""
     import torch
     from lbw_amd import attention_fp8kv, attention_segments, cross_attention, quantize_kv_fp8
     g = torch.Generator(device=dev).manual_seed(99)
     rnd = lambda *s: torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)
     out = {}
+    # q pre-scaled as the fused q/k kernel writes it in the layer pipeline (the folded softmax,
+    # as in the headline step), and the same call on a plain-scaled q
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, prescaled_q_scale
     for name, h, lq, lc in (("wan13b_480p_3f_over_6f", 12, 4680, 9360),
                             ("wan14b_480p_3f_over_18f", 40, 4680, 28080)):
         q = rnd(1, lq, h, D)
+        qs = (q.float() * prescaled_q_scale(D)).to(torch.bfloat16)
         kc, vc, kn, vn = rnd(1, lc, h, D), rnd(1, lc, h, D), rnd(1, lq, h, D), rnd(1, lq, h, D)
         o = torch.empty_like(q)
-        ms = _time_ms(lambda: attention_segments(q, [(kc, vc), (kn, vn)], out=o))
+        ms = _time_ms(lambda: attention_segments(qs, [(kc, vc), (kn, vn)], out=o,
+                                                 softmax_scale=PRESCALED_SOFTMAX_SCALE))
+        ms_plain = _time_ms(lambda: attention_segments(q, [(kc, vc), (kn, vn)], out=o))
         fl = 4.0 * lq * (lc + lq) * D * h
         out[name] = {"ms": round(ms, 4), "TFLOP/s": round(fl / ms / 1e9, 1),
-                     "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2)}
-        del q, kc, vc, kn, vn
+                     "pct_bf16_peak": round(fl / ms / 1e9 / PEAK_BF16_TFLOPS * 100, 2),
+                     "ms_plain_scale_q": round(ms_plain, 4),
+                     "pct_bf16_peak_plain_scale_q": round(fl / ms_plain / 1e9 / PEAK_BF16_TFLOPS * 100, 2)}
+        del q, qs, kc, vc, kn, vn
     q = rnd(1, 4680, 40, D)
     kx, vx = rnd(1, 512, 40, D), rnd(1, 512, 40, D)
     kl = torch.tensor([300], dtype=torch.int32, device=dev)
@@ -298,7 +308,6 @@ def other_configs(dev):
     del q, kx, vx
     # q pre-scaled as the fused q/k kernel writes it (the folded softmax), as in the headline
     # step; the same call on a plain-scaled q, and on a bf16 cache of the same keys
-    from lbw_amd import PRESCALED_SOFTMAX_SCALE, prescaled_q_scale
     q = rnd(1, 3600, 40, D)
     qs = (q.float() * prescaled_q_scale(D)).to(torch.bfloat16)
     lk = 3600 * 25
