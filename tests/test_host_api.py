@@ -41,3 +41,18 @@ def test_cpu_tensors_are_rejected_loudly():
     q, k, v = _qkv()
     with pytest.raises(RuntimeError, match="GPU tensor"):
         attention(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 (or a multi-rank launch) exits with status 2 and
+    says so, before touching a device."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for argv, env in ((["--gpus", "2"], {}), ([], {"WORLD_SIZE": "2"})):
+        r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), *argv],
+                           capture_output=True, text=True, timeout=120,
+                           env={**os.environ, **env})
+        assert r.returncode == 2, (argv, env, r.stdout, r.stderr)
+        assert "one GPU" in r.stdout + r.stderr
