@@ -1,12 +1,14 @@
 """Seeded random shapes through the fp8-KV attention kernel (Q K^T on the fp8 matrix cores, V
 staged and converted per wave): batch 1-2, 1-3 heads, 1-513 queries, 1-4 ragged fp8 segments
 (lengths around the 32-key sub-block and the 64-token scale block), random windows (empty ones
-included), 0-5 KV splits, q rows of magnitudes 2^-8 .. 2^2, V with 1 % outliers.
+included), 0-5 KV splits, q rows of magnitudes 2^-8 .. 2^2, V with 1 % outliers; every other
+case with q pre-scaled by log2(e)/sqrt(128) and softmax scale ln 2 (the folded instances).
 
 Against the oracle on the dequantised K/V: the fp32 output within the row bound its arithmetic
 fixes (P's bf16 rounding plus the fp8 matrix cores' score error, see test_gpu_fp8), and the bf16
 output equal to the round-to-nearest-even of the fp32 one (the same kernel, plan and merge; only
 the output type differs)."""
+import math
 import random
 
 import pytest
@@ -51,15 +53,21 @@ def test_fp8_random_shape_within_kernel_bound(lib, i):
         kds.append(O.dequantize_kv_fp8(kq.codes.cpu(), kq.scales.cpu()))
         vds.append(O.dequantize_kv_fp8(vq.codes.cpu(), vq.scales.cpu()))
     lo, hi = (None, None) if win is None else win
+    scale, kw = 128 ** -0.5, {}
+    if i % 2 == 1:
+        from lbw_amd import PRESCALED_SOFTMAX_SCALE, prescaled_q_scale
+        q = (q.float() * prescaled_q_scale(128)).to(torch.bfloat16)
+        scale, kw = math.log(2.0), {"softmax_scale": PRESCALED_SOFTMAX_SCALE}
     qd = q.to(DEV)
-    o32 = attention_fp8kv(qd, segs, kv_lo=lo, kv_hi=hi, num_splits=splits, out_dtype=torch.float32)
-    o16 = attention_fp8kv(qd, segs, kv_lo=lo, kv_hi=hi, num_splits=splits)
+    o32 = attention_fp8kv(qd, segs, kv_lo=lo, kv_hi=hi, num_splits=splits, out_dtype=torch.float32,
+                          **kw)
+    o16 = attention_fp8kv(qd, segs, kv_lo=lo, kv_hi=hi, num_splits=splits, **kw)
     torch.cuda.synchronize()
     kd, vd = torch.cat(kds, 1), torch.cat(vds, 1)
-    ref = O.attention_ref(q, kd, vd, kv_lo=lo, kv_hi=hi)
+    ref = O.attention_ref(q, kd, vd, kv_lo=lo, kv_hi=hi, softmax_scale=scale)
     a, b = (0, sum(lens)) if win is None else win
     if b > a:
-        bound = _row_bound(vd[:, a:b], _score_err(q, kd[:, a:b], 128 ** -0.5))
+        bound = _row_bound(vd[:, a:b], _score_err(q, kd[:, a:b], scale))
     else:
         bound = torch.full((B, Lq, H), 1e-5)   # no keys: the output is exactly 0
     err = (o32.cpu() - ref).abs().amax(-1)
