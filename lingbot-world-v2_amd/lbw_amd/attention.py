@@ -179,8 +179,11 @@ def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=Non
     the reference passes them -- one-element tensors on the device (``attn_lo``,
     ``attn_hi``) -- the kernel reads them there and the call never synchronises the host.
     ``q_lens``/``k_lens`` are ignored with the reference's warning (attention.py:1128-1132);
-    masked cross-attention is ``cross_attention``. ``q_scale`` is ignored, as the reference
-    ignores it on every path (attention.py:1082-1143), with a warning. The kernels compute in
+    masked cross-attention is ``cross_attention``. ``q_scale`` and ``softmax_scale`` are
+    ignored, as the reference ignores them on every path (attention.py:1082-1143: its kernels
+    and its SDPA fallback use 1/sqrt(head_dim), attention.py:378, 439), with a warning; a caller
+    that wants another scale, or the folded softmax of a pre-scaled q, calls
+    ``attention_segments``. The kernels compute in
     bf16, so ``dtype`` must be ``torch.bfloat16`` (the reference computes in ``dtype``; any
     other value raises). Output: bf16 ``[B, Lq, N, D]``."""
     _check_dtype(dtype)
@@ -197,11 +200,15 @@ def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=Non
     if q_scale is not None:
         warnings.warn("q_scale is ignored, as in the reference's attention() "
                       "(wan/modules/attention.py:1082-1143)")
+    if softmax_scale is not None:
+        warnings.warn("softmax_scale is ignored, as in the reference's attention(): the scale is "
+                      "1/sqrt(head_dim) (wan/modules/attention.py:1082-1143); attention_segments "
+                      "takes one")
     lo, hi = kv_lo, kv_hi
     if attn_mask is not None and lo is None and hi is None:
         lo, hi = window_from_mask(attn_mask, k.shape[1])
     on_dev = any(torch.is_tensor(b) and b.device.type != "cpu" for b in (lo, hi))
-    out = attention_segments(q, [(k, v)], kv_lo=lo, kv_hi=hi, softmax_scale=softmax_scale,
+    out = attention_segments(q, [(k, v)], kv_lo=lo, kv_hi=hi,
                              cross=bool(is_cross_attn) and k.shape[1] <= 4096 and not on_dev)
     return out
 

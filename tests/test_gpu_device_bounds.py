@@ -139,6 +139,23 @@ def test_q_scale_is_ignored_like_the_reference(lib):
     assert torch.equal(a, b)
 
 
+def test_softmax_scale_is_ignored_like_the_reference(lib):
+    """The reference's attention() scales by 1/sqrt(head_dim) whatever softmax_scale says (its
+    kernels and its SDPA fallback, attention.py:378, 439, 1127-1143): the drop-in returns the
+    same result, with a warning, and equals the oracle at the default scale."""
+    from lbw_amd import attention
+    q, k, v = _case(1, 64, 2, 300, seed=4)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        a = attention(qd, kd, vd, softmax_scale=0.25)
+    assert any("softmax_scale" in str(x.message) for x in w)
+    b = attention(qd, kd, vd)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert_parity(a, O.attention_ref(q, k, v))
+
+
 def test_cross_attention_refuses_device_bounds(lib):
     from lbw_amd import attention_segments
     q, k, v = _case(1, 64, 2, 300, seed=2)
