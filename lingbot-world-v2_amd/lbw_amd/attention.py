@@ -221,14 +221,31 @@ def exact_attention(q, k, v, dtype=torch.bfloat16):
     return attention(q, k, v, dtype=dtype)
 
 
+def _nmajor_chunk(kc, vc, d):
+    """One N-major cache chunk as the reference passes it to its merged path
+    (attention.py:1016-1019): K ``[N, D, L]`` (pre-transposed) or ``[N, L, D]`` (told apart as
+    there: the last dim is D and the middle one is not), V ``[N, L, D]``; returned as
+    ``[1, L, N, D]`` views of the same memory (K d-major in the first case)."""
+    if kc.dim() != 3 or vc.dim() != 3:
+        raise ValueError("N-major chunks are 3-D: K [N, D, L] or [N, L, D], V [N, L, D]")
+    tp_k = int(kc.shape[-1]) == d and int(kc.shape[1]) != d
+    k4 = kc.permute(1, 0, 2)[None] if tp_k else kc.permute(2, 0, 1)[None]
+    return k4, vc.permute(1, 0, 2)[None]
+
+
 def exact_attention_chunks(q, k_chunks, v_chunks, dtype=torch.bfloat16):
     """attention.py:1048-1058: attention over the concatenation of KV chunks, read in
-    place as segments (no torch.cat, no padding copy). Chunks are ``[B, L_c, N, D]``.
+    place as segments (no torch.cat, no padding copy). Chunks are ``[B, L_c, N, D]``, or, as
+    the reference's merged path takes them, N-major 3-D chunks (K ``[N, D, L]`` or
+    ``[N, L, D]``, V ``[N, L, D]``; q ``[1, Lq, N, D]``), read where they lie.
     ``dtype`` must be bf16, as for :func:`attention`."""
     _check_dtype(dtype)
     if len(k_chunks) != len(v_chunks):
         raise ValueError("k_chunks and v_chunks differ in length")
-    return attention_segments(q, list(zip(k_chunks, v_chunks)))
+    pairs = list(zip(k_chunks, v_chunks))
+    if pairs and pairs[0][0].dim() == 3:
+        pairs = [_nmajor_chunk(kc, vc, q.shape[-1]) for kc, vc in pairs]
+    return attention_segments(q, pairs)
 
 
 def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16, n_distinct=None):
@@ -253,7 +270,7 @@ def cross_attention_dedup(q, k, v, bias, kc, dtype=torch.bfloat16):
     ``dtype`` must be bf16, as for :func:`attention`."""
     _check_dtype(dtype)
     if k.dim() == 3 and v.dim() == 3:   # the reference's N-major cache itself: [N, D, L], [N, L, D]
-        k, v = k.permute(2, 0, 1)[None], v.permute(1, 0, 2)[None]
+        k, v = _nmajor_chunk(k, v, q.shape[-1])
     kc = int(kc)
     if bias.numel() != kc:
         raise ValueError(f"bias has {bias.numel()} values, kc = {kc}")

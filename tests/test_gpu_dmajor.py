@@ -132,6 +132,28 @@ def test_dmajor_cache_written_by_the_qk_kernel(lib):
     assert_parity(out, ref, "d-major cache")
 
 
+def test_exact_attention_chunks_nmajor(lib):
+    """exact_attention_chunks over the reference's N-major chunk list (attention.py:1048-1058,
+    993-1019): K [N, D, L] (pre-transposed) or [N, L, D], V [N, L, D], chunks of different
+    lengths read where they lie; against the oracle over the concatenation."""
+    from lbw_amd import exact_attention_chunks
+    g = torch.Generator().manual_seed(12)
+    H, D, Lq = 3, 128, 333
+    lens = [1560, 64, 936]
+    q = torch.randn(1, Lq, H, D, generator=g).to(torch.bfloat16)
+    ks = [torch.randn(1, L, H, D, generator=g).to(torch.bfloat16) for L in lens]
+    vs = [(0.5 * torch.randn(1, L, H, D, generator=g)).to(torch.bfloat16) for L in lens]
+    ref = O.attention_ref(q, torch.cat(ks, 1), torch.cat(vs, 1))
+    v_n = [v[0].permute(1, 0, 2).contiguous().to(DEV) for v in vs]          # [N, L, D]
+    for k_layout in ("ndl", "nld"):
+        if k_layout == "ndl":
+            k_n = [k[0].permute(1, 2, 0).contiguous().to(DEV) for k in ks]  # [N, D, L]
+        else:
+            k_n = [k[0].permute(1, 0, 2).contiguous().to(DEV) for k in ks]  # [N, L, D]
+        out = exact_attention_chunks(q.to(DEV), k_n, v_n)
+        assert_parity(out, ref, f"N-major chunks, K {k_layout}")
+
+
 def test_dmajor_refusals(lib):
     from lbw_amd import attention_fp8kv, attention_segments, quantize_kv_fp8
     q, ks, vs = _case(1, 64, 2, [100, 64], seed=1)
