@@ -254,10 +254,14 @@ def cross_attention(q, k, v, k_lens=None, dtype=torch.bfloat16, n_distinct=None)
     ``k_lens=None`` reproduces that). ``n_distinct`` selects the exact deduplicated form of
     attention.py:493-554: rows ``n_distinct..`` of k/v are identical (the context's padding)
     and are attended as one key weighted by their count (see ``padding_start``).
-    ``dtype`` must be bf16, as for :func:`attention`."""
+    k / v are ``[B, L, N, D]`` or, for batch 1, the reference's N-major cross cache as
+    cte_cross_attention_nmajor takes it (attention.py:557-579: K ``[N, D, L]``, V ``[N, L, D]``),
+    read in place. ``dtype`` must be bf16, as for :func:`attention`."""
     _check_dtype(dtype)
     if n_distinct is not None and k_lens is not None:
         raise ValueError("dedup reproduces the unmasked attention: pass k_lens or n_distinct")
+    if k.dim() == 3 and v.dim() == 3:
+        k, v = _nmajor_chunk(k, v, q.shape[-1])
     return attention_segments(q, [(k, v)], k_lens=k_lens, cross=True, n_distinct=n_distinct)
 
 

@@ -96,6 +96,11 @@ def test_nmajor_cross_cache_dedup(lib):
     kl = torch.tensor([300], dtype=torch.int32, device=DEV)
     out_m = cross_attention(q.to(DEV), k_nd, v_nld, k_lens=kl)
     assert_parity(out_m, O.attention_ref(q, k, v, k_lens=torch.tensor([300])), "masked")
+    # the same cache as the 3-D N-major tensors the reference's cross path passes
+    k3 = k[0].permute(1, 2, 0).contiguous().to(DEV)      # [N, D, L]
+    v3 = v[0].permute(1, 0, 2).contiguous().to(DEV)      # [N, L, D]
+    out3 = cross_attention(q.to(DEV), k3, v3)
+    assert_parity(out3, O.attention_ref(q, k, v), "N-major 3-D")
 
 
 def test_dmajor_cache_written_by_the_qk_kernel(lib):
