@@ -281,12 +281,26 @@ int run_attention(const lbw_attn_params* p, bool fp8, void* ws, size_t ws_bytes,
   hipStream_t st = static_cast<hipStream_t>(stream);
   // Cross-attention: the persistent kernel whenever the keys may fit its LDS-resident chunk
   // (per-batch k_lens are only known on the device; longer batches run there in chunks). A
-  // context the host knows to be longer goes to the chunk kernel as a single pass, which
-  // streams it faster than the cross kernel's chunk reloads.
-  if (cross && a.k_lens == nullptr && a.hi - a.lo > cross_attn_max_keys_resident()) cross = false;
-  // (the cross kernel reads K token-major and takes no general bias: such a context runs the
+  // context the host knows to be longer, every key attended (the reference's unmasked 512-row
+  // call), streams through the ring form; a longer one with the dedup's multiplicity bias goes
+  // to the chunk kernel as a single pass.
+  // (the cross kernels read K token-major and take no general bias: such a context runs the
   // chunk kernel, one pass)
   if (cross && (a.k_dmajor || a.key_bias != nullptr)) cross = false;
+  bool ring = false;
+  if (cross && a.k_lens == nullptr && a.hi - a.lo > cross_attn_max_keys_resident()) {
+    cross = false;
+    ring = a.mult_key < 0;
+  }
+  if (ring) {
+    // Q and O rows of one (batch, head) are addressed with 31-bit byte offsets
+    const int64_t rows = (int64_t)p->lq + 512;
+    if (rows * p->q_stride_l * 2 >= (int64_t(1) << 31) || rows * p->o_stride_l * 4 >= (int64_t(1) << 31))
+      return fail(LBW_ERR_UNSUPPORTED, "cross-attention: q/out rows span more than 2 GiB");
+    hipError_t e = launch_cross_ring(a, num_cus(), st);
+    if (e != hipSuccess) return hip_fail(e, "cross-attention ring kernel launch");
+    return LBW_OK;
+  }
   if (cross) {
     // one segment, single pass: the persistent cross-attention kernel; its chunk loads address
     // up to 320 rows with 32-bit offsets from the chunk's first row

@@ -3,7 +3,8 @@ dedup entry point) against the fp32 oracle.
 
 The kernel keeps a (batch, head)'s K/V rows resident in LDS when at most 320 keys are attended
 and otherwise walks them in 320-key chunks, with persistent workgroups that run consecutive
-256-query rounds. The cases cover both paths and their edges: key counts around the 32-key
+256-query rounds; an unmasked context longer than 320 keys runs its ring form, which streams the
+context through LDS in 64-key tiles and pipelines each round into the next. The cases cover both paths and their edges: key counts around the 32-key
 sub-block and the 320-key chunk, per-batch valid lengths (k_lens) that put one batch on each
 path, windows, query counts that leave partial 32-query blocks and rounds, head counts whose
 rounds straddle workgroups, strided views, the bf16 bar and, on the fp32 output, the bound the
@@ -90,8 +91,9 @@ def test_cross_rounds_across_workgroups_fp32(lib, H, Lq):
 ])
 def test_cross_long_unmasked_context(lib, B, Lq, H, L, window):
     """Unmasked contexts longer than the 320 resident keys (up to the reference's padded 512)
-    run the chunk kernel as one pass: bf16 bar, and the fp32 output within the kernel's
-    arithmetic bound and equal to the bf16 output before its rounding."""
+    run the ring form (the context streamed through LDS, rounds pipelined into each other):
+    bf16 bar, and the fp32 output within the kernel's arithmetic bound and equal to the bf16
+    output before its rounding."""
     from lbw_amd import attention_segments, cross_attention
     q, k, v = _qkv(B, Lq, H, L, seed=3 * Lq + L + H, qgain=2.0)
     lo, hi = (None, None) if window is None else window
@@ -109,6 +111,59 @@ def test_cross_long_unmasked_context(lib, B, Lq, H, L, window):
     err = float((o32.cpu() - ref).abs().max())
     assert err <= _kernel_bound(v[:, a:b]), err
     assert torch.equal(o32.to(torch.bfloat16), out)
+
+
+@pytest.mark.parametrize("H,Lq,L", [(40, 4680, 512), (3, 25600, 448), (1, 200, 330)])
+def test_cross_ring_rounds_fp32(lib, H, Lq, L):
+    """The ring form over many rounds per workgroup (25600 queries of 3 heads: ~10 rounds each),
+    rounds crossing heads, a workgroup with a single round (one head of 200 queries), and the
+    round boundary at every stage of the ring (8 and 7 tiles per round): fp32 output against the
+    arithmetic bound on sampled rows of several heads, including the partial last 32-query
+    block, with peaked queries (gain 4) so that the exponent reference moves; bf16 output equal
+    to the fp32 output rounded once."""
+    from lbw_amd import attention_segments, cross_attention
+    q, k, v = _qkv(1, Lq, H, L, seed=H + L, qgain=4.0)
+    print(f"case H={H} Lq={Lq} L={L}", flush=True)
+    dq, dk, dv = q.to(DEV), k.to(DEV), v.to(DEV)
+    o32 = attention_segments(dq, [(dk, dv)], cross=True, out_dtype=torch.float32)
+    o16 = cross_attention(dq, dk, dv)
+    torch.cuda.synchronize()
+    assert torch.equal(o32.to(torch.bfloat16), o16)
+    tail = torch.arange((Lq // 32) * 32, Lq)
+    sel = torch.cat([torch.randperm(Lq, generator=torch.Generator().manual_seed(L))[:300], tail])
+    sel = sel.unique().sort().values
+    oc = o32[:, sel].cpu()
+    for h in sorted({0, H // 2, H - 1}):
+        ref = O.attention_ref(q[:, sel][:, :, h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1])
+        err = float((oc[:, :, h:h + 1] - ref).abs().max())
+        bound = _kernel_bound(v[:, :, h])
+        assert err <= bound, (h, err, bound)
+
+
+def test_cross_ring_rounds_restart_the_softmax(lib):
+    """Each round of the ring form starts a fresh softmax: 256-query rounds alternate between
+    queries scaled by 40 and by 1/40 (scores ~1e3 against ~1e-1), so a reference carried over
+    from a large round would underflow the next round's probabilities to 0."""
+    from lbw_amd import cross_attention
+    q, k, v = _qkv(1, 2048, 2, 512, seed=91)
+    gain = torch.where((torch.arange(2048) // 256) % 2 == 0, 40.0, 1.0 / 40.0)
+    q = (q.float() * gain[None, :, None, None]).to(torch.bfloat16)
+    out = cross_attention(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert_parity(out, O.attention_ref(q, k, v), "alternating rounds")
+
+
+def test_cross_ring_non_finite_value_stays_in_its_head(lib):
+    """An infinite V entry in one head makes that head's outputs non-finite (as the reference's
+    softmax(QK^T) V does) and leaves every other head's outputs exact: the round boundary adds
+    only the previous round's own P V to the previous round's O."""
+    from lbw_amd import cross_attention
+    q, k, v = _qkv(1, 1024, 4, 512, seed=5)
+    v[:, 77, 1, 5] = float("inf")
+    out = cross_attention(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
+    assert not torch.isfinite(out[:, :, 1, 5]).any()
+    keep = [0, 2, 3]
+    assert_parity(out[:, :, keep], O.attention_ref(q[:, :, keep], k[:, :, keep], v[:, :, keep]),
+                  "other heads")
 
 
 def test_cross_dedup_past_the_resident_keys(lib):

@@ -134,6 +134,41 @@ def test_prescaled_cross_attention_masked_and_dedup(lib):
     assert_parity(out, O.attention_ref(q[:1], kd, vd, softmax_scale=LN2), "dedup")
 
 
+@pytest.mark.parametrize("H,Lq,L,gain", [(40, 4680, 512, 4.0), (3, 9000, 448, 1.0), (2, 700, 330, 8.0)])
+def test_prescaled_cross_ring(lib, H, Lq, L, gain):
+    """The folded softmax in the cross ring form (an unmasked context over 320 keys): rounds that
+    restart the exponent reference without rescaling the previous round's O, peaked queries that
+    move it mid-round; fp32 output within the arithmetic bound on sampled rows of three heads, the
+    bf16 output equal to it rounded once and within twice that bound (plus the bf16 rounding) of
+    the plain-softmax kernel on the same inputs."""
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments
+    g = torch.Generator().manual_seed(L + H)
+    q = _prescaled((gain * torch.randn(1, Lq, H, 128, generator=g)).to(torch.bfloat16))
+    k = torch.randn(1, L, H, 128, generator=g).to(torch.bfloat16)
+    v = (0.5 * torch.randn(1, L, H, 128, generator=g)).to(torch.bfloat16)
+    print(f"case H={H} Lq={Lq} L={L} gain={gain}", flush=True)
+    dq, dk, dv = q.to(DEV), k.to(DEV), v.to(DEV)
+    o32 = attention_segments(dq, [(dk, dv)], cross=True, softmax_scale=PRESCALED_SOFTMAX_SCALE,
+                             out_dtype=torch.float32)
+    o16 = attention_segments(dq, [(dk, dv)], cross=True, softmax_scale=PRESCALED_SOFTMAX_SCALE)
+    plain = attention_segments(dq, [(dk, dv)], cross=True, softmax_scale=LN2 * (1 + 2.0 ** -21))
+    torch.cuda.synchronize()
+    assert torch.equal(o32.to(torch.bfloat16), o16)
+    # (the two forms round p differently, each within the arithmetic bound of the exact result:
+    # together within twice it, plus the bf16 rounding of both outputs)
+    tol = 2 * float(v.float().abs().max()) * 2.0 ** -8 * 1.01 + 2.0 ** -8 * float(plain.float().abs().max())
+    assert float((o16.float() - plain.float()).abs().max()) <= tol
+    sel = torch.cat([torch.randperm(Lq, generator=torch.Generator().manual_seed(3))[:300],
+                     torch.arange((Lq // 32) * 32, Lq)]).unique().sort().values
+    oc = o32[:, sel].cpu()
+    for h in sorted({0, H // 2, H - 1}):
+        ref = O.attention_ref(q[:, sel][:, :, h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1],
+                              softmax_scale=LN2)
+        err = float((oc[:, :, h:h + 1] - ref).abs().max())
+        bound = float(v[:, :, h].float().abs().max()) * 2.0 ** -8 * 1.01 + 1e-5
+        assert err <= bound, (h, err, bound)
+
+
 def test_prescaled_partials_and_chain(lib):
     """The partials API (tracked row max, the FMA form with c = 1) under the pre-scaled pairing:
     m in scaled units (scale * s) as the oracle's partials, and a chain over key sets equal to
