@@ -83,7 +83,7 @@ hipError_t launch_attn_merge(const MergeKernelArgs& a, hipStream_t stream);
 hipError_t launch_cross_attn(const AttnKernelArgs& a, int num_cus, hipStream_t stream);
 int cross_attn_max_keys_resident();
 // The ring form (cross_attn.hip): every key of [lo, hi) attended (no k_lens, no multiplicity
-// bias), 64 < hi - lo <= 4096; the context streams through an LDS ring, persistent workgroups.
+// bias), 320 < hi - lo <= 4096; the context streams through an LDS ring, persistent workgroups.
 hipError_t launch_cross_ring(const AttnKernelArgs& a, int num_cus, hipStream_t stream);
 
 struct QkNormRopeArgs {

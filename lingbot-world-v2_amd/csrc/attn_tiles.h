@@ -46,8 +46,19 @@ __device__ __forceinline__ u32x2 lds_read_b64(int addr) {
 // insertion treats an in-flight builtin copy as a hazard for every later LDS transpose read and
 // waits for all copies before each one, which would serialise the prefetch. The kernel waits
 // for the tiles it reads itself (wait_tiles_outstanding, then a barrier).
+// The compiler does not insert the wait states an instruction inside inline asm needs: a vector
+// memory instruction must not read an SGPR within 5 wait states of a VALU write of it (such as
+// a v_readlane reload of a spilled SGPR, or a v_readfirstlane). The build checks the assembly of
+// every kernel for that (check_dma_hazards.py); a copy it flags takes dma16_guarded.
 __device__ __forceinline__ void dma16(const unsigned char* sbase, uint32_t voff, uint32_t lds_dst) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_dst) : "memory");
+}
+// dma16 with the 5 wait states ahead of the copy (where the base may have been written by a
+// VALU instruction just before)
+__device__ __forceinline__ void dma16_guarded(const unsigned char* sbase, uint32_t voff,
+                                              uint32_t lds_dst) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_dst)
+               : "memory");
 }
 // 4 bytes per lane from a per-lane 64-bit address (global_load_lds_dword): lane l's dword lands
 // at LDS byte address lds_dst + 4 l.

@@ -463,7 +463,8 @@ constexpr int GNDMA = GTILE / (XW * 64 * 16); // 16-byte copies per lane per K (
 static_assert(GLDS <= 160 * 1024, "ring, Q rows and V ring must fit the LDS");
 static_assert(GNDMA == 2, "two 1 KB blocks of each tile per wave");
 
-// A 64-bit pointer that is the same in every lane, held in scalar registers (the copies' base).
+// A 64-bit pointer that is the same in every lane, held in scalar registers (the copies' base;
+// written by v_readfirstlane, so the copies that read it take dma16_guarded).
 __device__ __forceinline__ const unsigned char* uniform_ptr(const unsigned char* p) {
   const uint64_t x = (uint64_t)(uintptr_t)p;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
@@ -493,8 +494,8 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
   const uint32_t ks = (uint32_t)(sg.ksl * 2), vs = (uint32_t)(sg.vsl * 2);  // row strides, bytes
   const float c = sreg(a.scale_log2);
   const int64_t lo = a.lo;
-  const int n = (int)(a.hi - a.lo);        // keys of every round (host: 64 < n <= 4096)
-  const int T = (n + BN - 1) / BN;         // tiles per round (>= 2)
+  const int n = (int)(a.hi - a.lo);        // keys of every round (host: 320 < n <= 4096)
+  const int T = (n + BN - 1) / BN;         // tiles per round (>= 6)
   const int vlast = n - BN * (T - 1);      // valid rows of a round's last tile
   const int vrow_last = vlast == BN ? ROWS_FULL : pack_rows(0, vlast, 255);
   const int NT = (r1 - r0) * T;            // tiles of the workgroup
@@ -570,16 +571,16 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
 #pragma unroll
       for (int i = 0; i < GNDMA; ++i) {
         const uint32_t row = (uint32_t)opaque(dma_row[i]);
-        dma16(kt, row * ks + dma_col[i], kdst + 1024 * i);
-        dma16(vt, row * vs + dma_col[i], vdst + 1024 * i);
+        dma16_guarded(kt, row * ks + dma_col[i], kdst + 1024 * i);
+        dma16_guarded(vt, row * vs + dma_col[i], vdst + 1024 * i);
       }
     } else {
       // rows past the context fetch its last key instead (masked to p = 0 in the softmax)
 #pragma unroll
       for (int i = 0; i < GNDMA; ++i) {
         const int r = dma_row[i] < vlast ? dma_row[i] : vlast - 1;
-        dma16(kt, (uint32_t)r * ks + dma_col[i], kdst + 1024 * i);
-        dma16(vt, (uint32_t)r * vs + dma_col[i], vdst + 1024 * i);
+        dma16_guarded(kt, (uint32_t)r * ks + dma_col[i], kdst + 1024 * i);
+        dma16_guarded(vt, (uint32_t)r * vs + dma_col[i], vdst + 1024 * i);
       }
     }
     if (++it == T) {
@@ -588,18 +589,18 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
       if (++ir < r1) copy_base();
     }
   };
-  // this wave's 32 Q rows of the round at x into its LDS rows (rows past Lq fetch row Lq - 1;
-  // their outputs are dropped by the store's range check)
-  auto issue_q = [&](const RPos& x) {
+  // this wave's 32 Q rows of the round at x into its LDS rows, 1 KB blocks i0 .. i0 + n - 1 of 8
+  // (rows past Lq fetch row Lq - 1; their outputs are dropped by the store's range check)
+  auto issue_q = [&](const RPos& x, int i0, int n) {
     const int qb = x.rr * XW + wave;
     const unsigned char* qg = uniform_ptr(reinterpret_cast<const unsigned char*>(a.q + a.qsb * x.b + a.qsh * x.h));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = i0; i < i0 + n; ++i) {
       const int row = 4 * i + (lane >> 4);
       int q = qb * 32 + row;
       q = q < a.Lq ? q : a.Lq - 1;
       const uint32_t col = (uint32_t)(((lane & 15) ^ swz(row)) << 4);
-      dma16(qg, (uint32_t)q * (uint32_t)(a.qsl * 2) + col, (uint32_t)qlds + 1024u * i);
+      dma16_guarded(qg, (uint32_t)q * (uint32_t)(a.qsl * 2) + col, (uint32_t)qlds + 1024u * i);
     }
   };
 
@@ -612,8 +613,7 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
 
   // ---- start: round r0's Q, tiles 0 and 1; the V sub-block the first step's PV reads (P = 0)
   // is zeroed (tile 2 is copied into that stage only after the first barrier)
-  issue_q(pos0);
-  RPos qpos = rpos_next(pos0);  // the round whose Q rows are copied next
+  issue_q(pos0, 0, 8);
   issue_tile(0);
   if (NT > 1) issue_tile(1);
   {
@@ -805,6 +805,10 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
   // Step B: softmax of tile g half 1, PV of tile g half 0, S of tile g+1 half 0 (with the next
   // round's Q when tile g is its round's last).
   // Between them: wait for tile g+1, barrier, refill tile g-1's stage with tile g+2.
+  // The next round's Q rows are copied in pairs of 1 KB blocks after the tile copies of tiles
+  // 1 .. 4 (a round has at least 6 tiles), so that the whole chip's Q reads do not come in one
+  // burst at the round's end, and the tile waits after them leave those 2 loads in flight (the
+  // loads complete in order; a wait with the round's stores outstanding waits for everything).
   int r = r0, t = 0;
   RPos cpos = pos0, ppos = pos0;  // rounds r and r - 1
   auto tile = [&](auto st_c, int g) {
@@ -820,7 +824,12 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
     }
     step(I<ST * GTILE + GHALF>{}, I<SP * GTILE + GHALF>{}, std::true_type{}, I<-1>{},
          I<ST * GTILE>{}, sA, sB, pA, pB, 0, vrow, first);
-    if (g + 1 < NT) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile g+1 (and any Q rows)
+    if (g + 1 < NT) {
+      if (t >= 2 && t <= 5 && !last && r + 1 < r1)
+        asm volatile("s_waitcnt vmcnt(2)" ::: "memory");  // tile g+1, not the 2 Q loads after it
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): tile g+1 and everything before it
+    }
     barrier_nofence();
     // (copies and stores are issued right after a barrier, ahead of the tile copy, so that the
     // next wait for a tile covers them too)
@@ -832,19 +841,10 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[db][e] = 0.0f;
     }
-    if (last && r + 1 < r1) {
-      // the next round's Q (copied a round ago) for step B's S, and the Q after it into LDS
-      read_q();
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the rows are read before the copy
-      if (r + 2 < r1) {
-        issue_q(qpos);
-        qpos = rpos_next(qpos);
-      }
-    } else if (g == 0 && r0 + 1 < r1) {
-      issue_q(qpos);
-      qpos = rpos_next(qpos);
-    }
+    // the next round's Q (copied during this round) for step B's S
+    if (last && r + 1 < r1) read_q();
     if (g + 2 < NT) issue_tile(SP);
+    if (t >= 1 && t <= 4 && r + 1 < r1) issue_q(rpos_next(cpos), 2 * (t - 1), 2);
     step(I<SN * GTILE>{}, I<ST * GTILE>{}, std::false_type{}, I<SN * GTILE + GHALF>{},
          I<ST * GTILE + GHALF>{}, sB, sA, pB, pA, 1, vrow, false);
     // (selects, not branches on the counters: they stay scalar registers)
@@ -918,6 +918,8 @@ static hipError_t launch_ring(const AttnKernelArgs& a, dim3 grid, hipStream_t st
 }
 
 hipError_t launch_cross_ring(const AttnKernelArgs& a, int num_cus, hipStream_t stream) {
+  // (a round copies the next round's Q during its tiles 1 .. 4 and reads it in its last)
+  if (a.hi - a.lo <= 5 * BN || a.hi - a.lo > 4096) return hipErrorInvalidValue;
   const int nqb = (a.Lq + 31) / 32;
   const int64_t rounds = (int64_t)a.B * a.H * ((nqb + XW - 1) / XW);
   int64_t g = rounds < num_cus ? rounds : num_cus;
