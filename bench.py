@@ -459,9 +459,11 @@ def counter_workload():
 def cross_workload():
     """The program the cross-attention profiles run: 5 calls each of the 14B 480p
     cross-attention (4680 q x 40 heads over a 512-row context, rows 300.. identical) masked to
-    300 rows, unmasked (512 keys) and the exact dedup, on seeded inputs."""
+    300 rows, unmasked (512 keys) and the exact dedup, on seeded inputs; then 5 calls of the
+    unmasked context through the general chunk kernel (the path it took before the ring form),
+    for comparison in the same trace."""
     import torch
-    from lbw_amd import cross_attention, padding_start
+    from lbw_amd import attention_segments, cross_attention, padding_start
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     g = torch.Generator(device=dev).manual_seed(0)
@@ -478,6 +480,8 @@ def cross_workload():
         cross_attention(q, k, v)
     for _ in range(5):
         cross_attention(q, k, v, n_distinct=nd)
+    for _ in range(5):
+        attention_segments(q, [(k, v)], num_splits=1)
     torch.cuda.synchronize()
     print("cross workload done", flush=True)
 

@@ -144,8 +144,9 @@ int lbw_attention_fwd_noalloc(const lbw_attn_params* p, void* stream);
 
 /* Cross-attention to a short context (one segment of <= 4096 keys, typically 512), with the
  * optional per-batch valid length p->k_lens. Single pass, no workspace. Up to 320 attended keys
- * stay resident in LDS per (batch, head) (the masked 300-row context); longer unmasked contexts
- * run the chunk kernel as a single pass. */
+ * stay resident in LDS per (batch, head) (the masked 300-row context); a longer context with
+ * every key attended (no k_lens: the reference's unmasked 512-row call) streams through an LDS
+ * tile ring that runs across the persistent workgroups' rounds. */
 int lbw_cross_attention_fwd(const lbw_attn_params* p, void* stream);
 
 /* Exact deduplicated cross-attention (no mask): keys n_distinct .. len-1 of the one segment
