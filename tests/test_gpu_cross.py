@@ -166,6 +166,28 @@ def test_cross_ring_non_finite_value_stays_in_its_head(lib):
                   "other heads")
 
 
+def test_cross_out_views(lib):
+    """Both cross kernels (resident: 300 keys via k_lens; ring: all 512) writing into given
+    outputs: a bf16 view whose rows start 8 bytes past a 16-byte boundary (the kernels' 8-byte
+    store form) and an fp32 view; each equal to the call's own fresh output, and nothing written
+    outside the view."""
+    from lbw_amd import attention_segments
+    q, k, v = _qkv(1, 700, 3, 512, seed=13)
+    dq, dk, dv = q.to(DEV), k.to(DEV), v.to(DEV)
+    for kl in (torch.tensor([300], dtype=torch.int32, device=DEV), None):
+        ref16 = attention_segments(dq, [(dk, dv)], k_lens=kl, cross=True)
+        ref32 = attention_segments(dq, [(dk, dv)], k_lens=kl, cross=True, out_dtype=torch.float32)
+        big16 = torch.full((1, 700, 3, 136), 7.0, dtype=torch.bfloat16, device=DEV)
+        big32 = torch.full((1, 700, 3, 136), 7.0, dtype=torch.float32, device=DEV)
+        o16, o32 = big16[..., 4:132], big32[..., 4:132]
+        attention_segments(dq, [(dk, dv)], k_lens=kl, cross=True, out=o16)
+        attention_segments(dq, [(dk, dv)], k_lens=kl, cross=True, out=o32)
+        torch.cuda.synchronize()
+        assert torch.equal(o16, ref16) and torch.equal(o32, ref32), kl
+        for big in (big16, big32):
+            assert bool((big[..., :4] == 7).all()) and bool((big[..., 132:] == 7).all())
+
+
 def test_cross_dedup_past_the_resident_keys(lib):
     """The exact dedup over a context whose distinct rows end past the resident chunk (400 of
     512: the distinct rows and the weighted identical ones up to their tile's end, 448 keys)
