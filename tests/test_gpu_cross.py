@@ -88,6 +88,8 @@ def test_cross_rounds_across_workgroups_fp32(lib, H, Lq):
     (1, 64, 5, 512, None),
     (2, 1000, 3, 512, (20, 470)),    # a 450-key window
     (1, 100, 7, 450, None),
+    (1, 333, 3, 1000, None),         # 16 tiles a round, the last 40 keys valid
+    (1, 200, 2, 4096, None),         # the longest context: 64 tiles a round
 ])
 def test_cross_long_unmasked_context(lib, B, Lq, H, L, window):
     """Unmasked contexts longer than the 320 resident keys (up to the reference's padded 512)
