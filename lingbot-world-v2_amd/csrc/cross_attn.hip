@@ -550,24 +550,24 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
   pos0.h = (r0 / rpb) % a.H;
   pos0.b = (r0 / rpb) / a.H;
 
-  // ---- the copy side: tile `it` of round `ir` (at ipos) is the next to be copied
+  // ---- the copy side: tile `it` of round `ir` (at ipos) is the next to be copied, its K and V
+  // rows from kt / vt (stepped by a tile's bytes; set from the round's position at a round change)
   int ir = r0, it = 0;
   RPos ipos = pos0;
-  const unsigned char* ik = nullptr;
-  const unsigned char* iv = nullptr;
+  const unsigned char* kt = nullptr;
+  const unsigned char* vt = nullptr;
   auto copy_base = [&]() {
-    ik = reinterpret_cast<const unsigned char*>(sg.k) +
+    kt = reinterpret_cast<const unsigned char*>(sg.k) +
          (sg.ksb * ipos.b + sg.ksh * ipos.h + sg.ksl * lo) * 2;
-    iv = reinterpret_cast<const unsigned char*>(sg.v) +
+    vt = reinterpret_cast<const unsigned char*>(sg.v) +
          (sg.vsb * ipos.b + sg.vsh * ipos.h + sg.vsl * lo) * 2;
   };
   copy_base();
+  const int t_full = vlast == BN ? T : T - 1;  // tiles of a round with every row valid
   auto issue_tile = [&](int stage) {
-    const unsigned char* kt = uniform_ptr(ik + (uint64_t)(uint32_t)it * (BN * ks));
-    const unsigned char* vt = uniform_ptr(iv + (uint64_t)(uint32_t)it * (BN * vs));
     const uint32_t kdst = (uint32_t)sreg((int)lds_wave) + stage * GTILE;
     const uint32_t vdst = kdst + GV0;
-    if (it + 1 < T || vlast == BN) {
+    if (it < t_full) {
 #pragma unroll
       for (int i = 0; i < GNDMA; ++i) {
         const uint32_t row = (uint32_t)opaque(dma_row[i]);
@@ -587,6 +587,9 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
       it = 0;
       ipos = rpos_next(ipos);
       if (++ir < r1) copy_base();
+    } else {
+      kt += BN * ks;
+      vt += BN * vs;
     }
   };
   // this wave's 32 Q rows of the round at x into its LDS rows, 1 KB blocks i0 .. i0 + n - 1 of 8
@@ -847,14 +850,11 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
     if (t >= 1 && t <= 4 && r + 1 < r1) issue_q(rpos_next(cpos), 2 * (t - 1), 2);
     step(I<SN * GTILE>{}, I<ST * GTILE>{}, std::false_type{}, I<SN * GTILE + GHALF>{},
          I<ST * GTILE + GHALF>{}, sB, sA, pB, pA, 1, vrow, false);
-    // (selects, not branches on the counters: they stay scalar registers)
-    const RPos nx = rpos_next(cpos);
-    ppos.b = last ? cpos.b : ppos.b;
-    ppos.h = last ? cpos.h : ppos.h;
-    ppos.rr = last ? cpos.rr : ppos.rr;
-    cpos.b = last ? nx.b : cpos.b;
-    cpos.h = last ? nx.h : cpos.h;
-    cpos.rr = last ? nx.rr : cpos.rr;
+    if (last) {
+      ppos = cpos;
+      cpos = rpos_next(cpos);
+    }
+    // (selects, not a branch on the counters: they stay scalar registers)
     r += last ? 1 : 0;
     t = last ? 0 : t + 1;
   };
