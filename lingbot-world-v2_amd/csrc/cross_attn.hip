@@ -447,10 +447,11 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_attn_kernel(const AttnKernel
 // copied through a 3-stage LDS ring exactly as the chunk kernel's tiles are (one barrier per tile:
 // wait for tile g + 1, barrier, refill tile g - 1's stage with tile g + 2), except that the ring
 // runs on across rounds: the next round's first tiles are in flight while a round ends. Each
-// wave's Q rows of the next round are copied into LDS (its own 8 KB) a round ahead, and the round
-// boundary is pipelined like any other step: the last tile's second step computes S of the next
-// round's first sub-block with the new Q, and the next round's first step, which starts a fresh
-// softmax, still adds the old round's last P V into the old O, which is then stored and cleared.
+// wave's Q rows of the next round are copied into LDS (its own 8 KB) during the round and read at
+// its last tile, and the round boundary is pipelined like any other step: the last tile's second
+// step computes S of the next round's first sub-block with the new Q, and the next round's first
+// step, which starts a fresh softmax, still adds the old round's last P V into the old O, which
+// is then stored and cleared.
 //
 // LDS: K tiles [0, 48 KB), the waves' Q rows [48, 112 KB), V tiles [112, 160 KB).
 constexpr int GST = 3;                        // ring stages
