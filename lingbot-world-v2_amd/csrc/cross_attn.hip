@@ -464,8 +464,9 @@ constexpr int GNDMA = GTILE / (XW * 64 * 16); // 16-byte copies per lane per K (
 static_assert(GLDS <= 160 * 1024, "ring, Q rows and V ring must fit the LDS");
 static_assert(GNDMA == 2, "two 1 KB blocks of each tile per wave");
 
-// A 64-bit pointer that is the same in every lane, held in scalar registers (the copies' base;
-// written by v_readfirstlane, so the copies that read it take dma16_guarded).
+// A 64-bit pointer that is the same in every lane, held in scalar registers (the Q copies' base;
+// written by v_readfirstlane, so the copies that read it take dma16_guarded; the tile copies'
+// bases are stepped by scalar adds and go through dma16, which the build's assembly check covers).
 __device__ __forceinline__ const unsigned char* uniform_ptr(const unsigned char* p) {
   const uint64_t x = (uint64_t)(uintptr_t)p;
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
@@ -572,16 +573,16 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
 #pragma unroll
       for (int i = 0; i < GNDMA; ++i) {
         const uint32_t row = (uint32_t)opaque(dma_row[i]);
-        dma16_guarded(kt, row * ks + dma_col[i], kdst + 1024 * i);
-        dma16_guarded(vt, row * vs + dma_col[i], vdst + 1024 * i);
+        dma16(kt, row * ks + dma_col[i], kdst + 1024 * i);
+        dma16(vt, row * vs + dma_col[i], vdst + 1024 * i);
       }
     } else {
       // rows past the context fetch its last key instead (masked to p = 0 in the softmax)
 #pragma unroll
       for (int i = 0; i < GNDMA; ++i) {
         const int r = dma_row[i] < vlast ? dma_row[i] : vlast - 1;
-        dma16_guarded(kt, (uint32_t)r * ks + dma_col[i], kdst + 1024 * i);
-        dma16_guarded(vt, (uint32_t)r * vs + dma_col[i], vdst + 1024 * i);
+        dma16(kt, (uint32_t)r * ks + dma_col[i], kdst + 1024 * i);
+        dma16(vt, (uint32_t)r * vs + dma_col[i], vdst + 1024 * i);
       }
     }
     if (++it == T) {
