@@ -625,7 +625,9 @@ __global__ void __launch_bounds__(XW * 64, 1) cross_ring_kernel(const AttnKernel
     const u32x4 z = {0u, 0u, 0u, 0u};
     *reinterpret_cast<u32x4*>(lds + GV0 + (GST - 1) * GTILE + GHALF + 16 * threadIdx.x) = z;
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  // Q and tile 0 (tile 1's 4 copies, issued last, may still be in flight: tile 0's wait covers
+  // them), and the zeroed sub-block
+  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
   barrier_nofence();
   read_q();
