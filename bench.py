@@ -378,9 +378,12 @@ def boundary_costs(dev):
     ``host_us`` = host time to issue one call while the GPU is busy with earlier work (what the
     boundary adds on the CPU), ``eager_us`` = wall time per call of back-to-back calls from an idle
     GPU to the last one's end (what a caller waiting on each call sees), ``gpu_us`` = GPU time
-    per call. For the c4 chunk attention and the 14B 480p cross-attention (300-row mask)."""
+    per call. For the c4 chunk attention, the same call through the no-alloc C entry point (whose
+    fixed 64 MiB scratch holds no split partials at this size, so it runs one pass), and the 14B
+    480p cross-attention (300-row mask)."""
+    import ctypes
     import torch
-    from lbw_amd import PRESCALED_SOFTMAX_SCALE, attention_segments, cross_attention
+    from lbw_amd import PRESCALED_SOFTMAX_SCALE, _lib, attention_segments, cross_attention
     g = torch.Generator(device=dev).manual_seed(3)
     rnd = lambda *s: torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)
     q = rnd(1, LQ, H, D)
@@ -389,9 +392,13 @@ def boundary_costs(dev):
     qx = rnd(1, 4680, 40, D)
     kx, vx = rnd(1, 512, 40, D), rnd(1, 512, 40, D)
     kl = torch.tensor([300], dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    p_na = _lib.attn_params(q, out, [(kc, vc)], softmax_scale=PRESCALED_SOFTMAX_SCALE)
     calls = {
         "chunk_attention_wan14b_720p": (lambda: attention_segments(
             q, [(kc, vc)], out=out, softmax_scale=PRESCALED_SOFTMAX_SCALE), 10),
+        "chunk_attention_wan14b_720p_noalloc": (lambda: _lib.check(
+            lib.lbw_attention_fwd_noalloc(ctypes.byref(p_na), _lib.stream_ptr()), "noalloc"), 10),
         "cross_attention_wan14b_480p_300valid": (lambda: cross_attention(qx, kx, vx, k_lens=kl), 50),
     }
     res = {}
