@@ -72,3 +72,21 @@ def test_hazard_through_a_branch(tmp_path):
 """
     assert _run(tmp_path, body) == 1
     assert _run(tmp_path, body.replace("\ts_cbranch_scc1 .LBB0_2\n", "\ts_nop 7\n\ts_cbranch_scc1 .LBB0_2\n")) == 0
+
+
+def test_every_source_with_inline_asm_copies_is_checked_by_the_build():
+    """Every kernel source that issues the inline-asm LDS copies (dma16 / dma4, or the
+    instruction itself) has its assembly in the Makefile's ASMS list, so the build checks it."""
+    import re
+    csrc = os.path.join(HERE, "..", "lingbot-world-v2_amd", "csrc")
+    mk = open(os.path.join(csrc, "Makefile")).read()
+    asms = re.search(r"^ASMS\s*:=(.*)$", mk, re.M).group(1)
+    checked = set(re.findall(r"(\w+)\.s\b", asms))
+    users = set()
+    for f in os.listdir(csrc):
+        if f.endswith(".hip"):
+            src = open(os.path.join(csrc, f)).read()
+            if re.search(r"\bdma16(_guarded)?\s*\(|\bdma4\s*\(|global_load_lds", src):
+                users.add(f[:-4])
+    assert users, "no source issues the copies: the pattern is stale"
+    assert users <= checked, f"not checked by the build: {sorted(users - checked)}"
