@@ -111,9 +111,18 @@ __device__ __forceinline__ QkTensor qk_tensor(const QkNormRopeArgs& a, const uin
   return u;
 }
 
+// 16 bytes of a row read once: NT, the non-temporal hint (the d-major kernel: its rows stream
+// past the caches, 17 % less time at the 14B 720p chunk; the rows kernel, whose outputs the
+// attention reads next, measured 7 % slower with it in the layer sequence and keeps plain loads)
+template <bool NT>
+__device__ __forceinline__ u32x4 qk_load16(const uint16_t* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  else return *reinterpret_cast<const u32x4*>(p);
+}
+
 // issue the loads of one tensor's row (kept apart from qk_one_norm so that a wave can have the
 // loads of several rows in flight)
-template <int NCH>
+template <int NCH, bool NT>
 __device__ __forceinline__ void qk_one_load(const QkNormRopeArgs& a, const QkTensor& u, int row,
                                             int lane, QkOne<NCH>& s) {
   const int nchunk = a.C / 8;
@@ -122,7 +131,7 @@ __device__ __forceinline__ void qk_one_load(const QkNormRopeArgs& a, const QkTen
   for (int i = 0; i < NCH; ++i) {
     const int ch = lane + 64 * i;
     if (i + 1 < NCH || ch < nchunk)  // only the last chunk can run past the row
-      s.x[i] = *reinterpret_cast<const u32x4*>(xr + 8 * ch);
+      s.x[i] = qk_load16<NT>(xr + 8 * ch);
   }
 }
 
@@ -220,8 +229,9 @@ __device__ __forceinline__ u32x4 qk_finish(const u32x4& x, const u32x4& bv, cons
   return ov;
 }
 
-// copy the chunks i of a V row with i % nsplit == part (the row's waves share the copy)
-template <int NCH>
+// copy the chunks i of a V row with i % nsplit == part (the row's waves share the copy); NT:
+// as for qk_load16, the stores too
+template <int NCH, bool NT>
 __device__ __forceinline__ void qk_copy_v(const QkNormRopeArgs& a, int row, int lane, int part,
                                           int nsplit) {
   const int nchunk = a.C / 8;
@@ -232,13 +242,14 @@ __device__ __forceinline__ void qk_copy_v(const QkNormRopeArgs& a, int row, int 
   for (int i = 0; i < NCH; ++i) {
     const int ch = lane + 64 * i;
     if (i % nsplit == part && (i + 1 < NCH || ch < nchunk))
-      xv[i] = *reinterpret_cast<const u32x4*>(vs + 8 * ch);
+      xv[i] = qk_load16<NT>(vs + 8 * ch);
   }
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int ch = lane + 64 * i;
     if (i % nsplit == part && (i + 1 < NCH || ch < nchunk))
-      *reinterpret_cast<u32x4*>(vd + 8 * ch) = xv[i];
+      if constexpr (NT) __builtin_nontemporal_store(xv[i], reinterpret_cast<u32x4*>(vd + 8 * ch));
+      else *reinterpret_cast<u32x4*>(vd + 8 * ch) = xv[i];
   }
 }
 
@@ -267,7 +278,7 @@ qk_norm_rope_kernel(const QkNormRopeArgs a) {
   for (int row = blockIdx.x * rows_per_block + wave / ntens; row < a.L;
        row += gridDim.x * rows_per_block) {
     QkOne<NCH> s;
-    qk_one_load<NCH>(a, u, row, lane, s);
+    qk_one_load<NCH, false>(a, u, row, lane, s);
     qk_one_norm<NCH>(a, tab, u, row, lane, s);
     uint16_t* o = u.o + u.os * row;
 #pragma unroll
@@ -279,7 +290,7 @@ qk_norm_rope_kernel(const QkNormRopeArgs a) {
                       *reinterpret_cast<const u32x4*>(u.gamma + 8 * ch), s.r, s.c, s.sn,
                       s.rotate, u.scale);
     }
-    if (a.v != nullptr) qk_copy_v<NCH>(a, row, lane, t, ntens);
+    if (a.v != nullptr) qk_copy_v<NCH, false>(a, row, lane, t, ntens);
   }
 }
 
@@ -317,7 +328,7 @@ qk_norm_rope_dmajor_kernel(const QkNormRopeArgs a) {
 #pragma unroll
   for (int k = 0; k < 2; ++k)
     if (k < nunit && tok0 + (QT_ROWS / 2) * k < nvalid)
-      qk_one_load<NCH>(a, u, t0 + tok0 + (QT_ROWS / 2) * k, lane, s[k]);
+      qk_one_load<NCH, true>(a, u, t0 + tok0 + (QT_ROWS / 2) * k, lane, s[k]);
 #pragma unroll
   for (int k = 0; k < 2; ++k)
     if (k < nunit && tok0 + (QT_ROWS / 2) * k < nvalid)
@@ -365,7 +376,7 @@ qk_norm_rope_dmajor_kernel(const QkNormRopeArgs a) {
     }
     __syncthreads();  // the slice is read before the next one is staged
   }
-  if (a.v != nullptr && wave < nvalid) qk_copy_v<NCH>(a, t0 + wave, lane, 0, 1);
+  if (a.v != nullptr && wave < nvalid) qk_copy_v<NCH, true>(a, t0 + wave, lane, 0, 1);
 }
 
 template <int NCH>
